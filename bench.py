@@ -1,0 +1,204 @@
+#!/usr/bin/env python3
+"""Benchmark of the gfx950 GEMM hot path (one MI355X).
+
+Headline (BASELINE.json metric): bf16 GEMM TFLOPS at 4096^3 (config 2: NN layout,
+N(0,1) inputs, fp32 accumulate, bf16 output) as a fraction of the dense bf16
+MFMA peak, plus the W4A16 decode GEMM (config 4: M=16, K=4096, N=11008, int4
+weights, group 128, zero point 8, bf16 out) in HBM GB/s against the HBM peak.
+
+A "step" is one launch of the GEMM over the 4096^3 problem with inputs already
+resident in HBM.  Kernel time is measured with HIP events on the stream the
+kernels are launched on (the t0mi runtime launches on torch's current stream).
+The W4A16 timing rotates over >= 512 MB of distinct weight copies so the
+256 MB Infinity Cache cannot serve repeats.
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--only gemm|w4a16] [--no-cpu]
+"""
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(ROOT, "rust-gpu_amd"))
+
+PEAK_BF16_TFLOPS = 2500.0   # MI355X dense bf16 MFMA (published)
+PEAK_HBM_GBS = 8000.0       # MI355X HBM3E (published)
+METRIC = "bf16 GEMM TFLOPS @4096³ (% MFMA peak); W4A16 decode HBM GB/s (% peak)"
+
+
+def parse():
+    p = argparse.ArgumentParser()
+    p.add_argument("--gpus", type=int, default=1)
+    p.add_argument("--steps", type=int, default=50)
+    p.add_argument("--warmup", type=int, default=10)
+    p.add_argument("--only", choices=["all", "gemm", "w4a16"], default="all")
+    p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    p.add_argument("--config", default=None, help="GEMM preset name to force (default: auto_select)")
+    return p.parse_args()
+
+
+def load_traffic(kernel_key):
+    """HBM bytes per launch from the committed rocprofv3 --pmc summary (FETCH_SIZE /
+    WRITE_SIZE, scaled by a copy-kernel calibration), or None if not measured."""
+    path = os.path.join(ROOT, "profiles", "traffic.json")
+    try:
+        with open(path) as f:
+            return json.load(f).get(kernel_key)
+    except (OSError, ValueError):
+        return None
+
+
+def bench_gemm(args, torch, t0mi, rt):
+    M = N = K = 4096
+    g = torch.Generator(device="cuda:0")
+    g.manual_seed(0x7402)
+    a = torch.randn(M, K, device="cuda:0", generator=g).to(torch.bfloat16)
+    b = torch.randn(K, N, device="cuda:0", generator=g).to(torch.bfloat16)
+    y = torch.empty(M, N, device="cuda:0", dtype=torch.bfloat16)
+    if args.config:
+        cfg = t0mi.preset(args.config)
+    else:
+        cfg = t0mi.auto_select(M, K, N)
+    cfg = cfg.copy(transpose=t0mi.NN, out_dtype=t0mi.OUT_BF16)
+    pa, pb, py = a.data_ptr(), b.data_ptr(), y.data_ptr()
+    for _ in range(args.warmup):
+        rt.gemm(cfg, pa, pb, py, M, N, K)
+    torch.cuda.synchronize()
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    t_host0 = time.perf_counter()
+    e0.record()
+    for _ in range(args.steps):
+        rt.gemm(cfg, pa, pb, py, M, N, K)
+    e1.record()
+    torch.cuda.synchronize()
+    t_host = time.perf_counter() - t_host0
+    ms = e0.elapsed_time(e1) / args.steps
+    flops = 2.0 * M * N * K
+    tflops = flops / (ms * 1e-3) / 1e12
+    print(f"[bench] gemm {cfg.name()} 4096^3 NN bf16-out: {ms*1e3:.1f} us/launch, {tflops:.1f} TFLOPS "
+          f"({100*tflops/PEAK_BF16_TFLOPS:.1f}% of peak); host wall {t_host:.3f}s", file=sys.stderr, flush=True)
+    return cfg, ms, tflops
+
+
+def bench_w4a16(args, torch, t0mi, rt):
+    Mw, Kw, Nw, G = 16, 4096, 11008, 128
+    wbytes = Kw // 8 * Nw * 4
+    sbytes = Kw // G * Nw * 2
+    copies = max(2, -(-512 * 1024 * 1024 // (wbytes + sbytes)))
+    g = torch.Generator(device="cuda:0")
+    g.manual_seed(0x7502)
+    a = torch.randn(Mw, Kw, device="cuda:0", generator=g).to(torch.bfloat16)
+    ws = [torch.randint(-2**31, 2**31 - 1, (Kw // 8, Nw), device="cuda:0", dtype=torch.int32, generator=g)
+          for _ in range(copies)]
+    ss = [(torch.rand(Kw // G, Nw, device="cuda:0", generator=g) * 0.015 + 0.005).to(torch.bfloat16)
+          for _ in range(copies)]
+    y = torch.empty(Mw, Nw, device="cuda:0", dtype=torch.bfloat16)
+    calls = max(args.steps * 4, 2 * copies)
+    for i in range(max(args.warmup, copies)):
+        rt.w4a16_gemm(a.data_ptr(), ws[i % copies].data_ptr(), ss[i % copies].data_ptr(), 0, 8, y.data_ptr(),
+                      Mw, Kw, Nw, G, t0mi.OUT_BF16)
+    torch.cuda.synchronize()
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for i in range(calls):
+        j = i % copies
+        rt.w4a16_gemm(a.data_ptr(), ws[j].data_ptr(), ss[j].data_ptr(), 0, 8, y.data_ptr(), Mw, Kw, Nw, G,
+                      t0mi.OUT_BF16)
+    e1.record()
+    torch.cuda.synchronize()
+    us = e0.elapsed_time(e1) * 1e3 / calls
+    alg_bytes = 2 * Mw * Kw + Kw * Nw // 2 + 2 * (Kw // G) * Nw + 2 * Mw * Nw
+    gbs = alg_bytes / (us * 1e-6) / 1e9
+    print(f"[bench] w4a16 decode 16x4096x11008 g128: {us:.2f} us/call, {gbs:.0f} GB/s "
+          f"({100*gbs/PEAK_HBM_GBS:.1f}% of HBM peak), {copies} weight copies rotated", file=sys.stderr, flush=True)
+    return us, gbs, alg_bytes, copies
+
+
+def cpu_baseline(which):
+    """The oracle (C restatement of cpu_gemm_nt_bf16, OpenMP over rows) timed on this host."""
+    import numpy as np
+    import oracle  # the CPU baseline leg is the only bench code that uses the oracle
+    threads = oracle.num_threads()
+    if which == "gemm":
+        M = N = K = 4096
+        rows = 1024
+        a = oracle.normal_bf16((rows, K), 0x7501, 0.0, 1.0)
+        b = oracle.normal_bf16((K, N), 0x7502, 0.0, 1.0)
+        t0 = time.perf_counter()
+        oracle.gemm_bf16(a, b, "nn")
+        dt = time.perf_counter() - t0
+        tflops = 2.0 * rows * N * K / dt / 1e12
+        return {"value": round(tflops, 4), "unit": "TFLOPS", "cores": threads, "kind": "port",
+                "sample": f"{rows} of 4096 rows of the 4096^3 NN GEMM ({dt:.1f} s), sequential fp32 per "
+                          f"output as cpu_gemm_nt_bf16 (src/t0/tile_ir.rs:5021-5038), OpenMP over rows"}
+    Mw, Kw, Nw, G = 16, 4096, 11008, 128
+    a = oracle.normal_bf16((Mw, Kw), 1, 0.0, 1.0)
+    w = oracle.pack_qweight(oracle.nibbles((Kw, Nw), 2))
+    s = oracle.uniform_bf16((Kw // G, Nw), 3, 0.005, 0.02)
+    t0 = time.perf_counter()
+    reps = 0
+    while True:
+        oracle.w4a16_gemm(a, w, s, None, G, 8)
+        reps += 1
+        if time.perf_counter() - t0 > 3.0:
+            break
+    dt = (time.perf_counter() - t0) / reps
+    alg_bytes = 2 * Mw * Kw + Kw * Nw // 2 + 2 * (Kw // G) * Nw + 2 * Mw * Nw
+    return {"value": round(alg_bytes / dt / 1e9, 3), "unit": "GB/s", "cores": threads, "kind": "port",
+            "sample": f"full 16x4096x11008 decode GEMM x{reps} ({dt*1e3:.0f} ms each): exact fp32 dequant "
+                      f"then the sequential-fp32 loop"}
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(f"bench.py: this build runs on one GPU only (asked for --gpus {args.gpus}); multi-GPU "
+              f"sharding of the GEMM path is described in DESIGN.md but not built.", file=sys.stderr)
+        sys.exit(2)
+    import torch
+    import t0mi
+    torch.cuda.init()
+    rt = t0mi.Runtime.on_torch_stream(0)
+    out = {"metric": METRIC, "n_gpus": 1, "steps": args.steps, "warmup": args.warmup, "higher_is_better": True,
+           "scaling": "weak", "vs_baseline": None, "dtype": "bf16", "data": "synthetic"}
+    if args.only in ("all", "gemm"):
+        cfg, ms, tflops = bench_gemm(args, torch, t0mi, rt)
+        out.update({"value": round(tflops, 2), "unit": "TFLOPS", "ms_per_step": round(ms, 5),
+                    "config": {"workload": "bf16 GEMM M=N=K=4096, A[M,K] x B[K,N] row-major (NN), N(0,1), "
+                                           "fp32 accumulate, bf16 out (BASELINE config 2)",
+                               "M": 4096, "N": 4096, "K": 4096, "kernel": cfg.name()}})
+        traffic = load_traffic("gemm_4096")
+        out["roofline"] = {"bound": "mfma", "achieved": round(tflops, 2), "peak": PEAK_BF16_TFLOPS,
+                           "unit": "TFLOP/s", "frac": round(tflops / PEAK_BF16_TFLOPS, 4), "traffic": traffic}
+    if args.only in ("all", "w4a16"):
+        us, gbs, alg_bytes, copies = bench_w4a16(args, torch, t0mi, rt)
+        w = {"value": round(gbs, 1), "unit": "GB/s", "us_per_call": round(us, 3),
+             "frac_of_peak": round(gbs / PEAK_HBM_GBS, 4), "algorithmic_bytes": alg_bytes,
+             "weight_copies_rotated": copies,
+             "workload": "W4A16 decode A[16,4096] bf16 x int4 W[4096,11008] g128 zp=8, bf16 out (BASELINE config 4)"}
+        out["w4a16_decode"] = w
+        out["roofline_w4a16"] = {"bound": "hbm", "achieved": round(gbs, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                                 "frac": round(gbs / PEAK_HBM_GBS, 4), "traffic": load_traffic("w4a16_decode")}
+        if args.only == "w4a16":
+            out.update({"value": round(gbs, 1), "unit": "GB/s", "ms_per_step": round(us * 1e-3, 6),
+                        "config": {"workload": w["workload"]}})
+    if not args.no_cpu:
+        try:
+            if args.only in ("all", "gemm"):
+                out["cpu_baseline"] = cpu_baseline("gemm")
+            if args.only in ("all", "w4a16"):
+                out["cpu_baseline_w4a16"] = cpu_baseline("w4a16")
+            if args.only == "w4a16":
+                out["cpu_baseline"] = out.pop("cpu_baseline_w4a16")
+        except Exception as e:  # the baseline is reported, never required
+            out["cpu_baseline"] = {"value": None, "error": str(e)}
+    rt.close()
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()

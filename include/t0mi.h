@@ -1,0 +1,242 @@
+/*
+ * t0mi.h — C ABI of the MI355X (gfx950) GEMM hot path.
+ *
+ * Drop-in replacement for the GEMM path of T0-GPU (clearnature/rust-gpu):
+ * the GemmConfig -> gemm_gen / tile_ir kernels, the auto-select and autotune
+ * entries, GpuKernel load/dispatch, and an INT4-dequant (W4A16) GEMM.  Every
+ * entry point below names the reference item it replaces (file:line in the
+ * reference tree).  Plain C types only: pointers, sizes and POD structs.
+ *
+ * Conventions
+ *  - Every function returning int returns T0MI_OK (0) or a negative T0MI_ERR_*.
+ *    The reference returns Result<_, String>; the string is available through
+ *    t0mi_last_error() (thread-local, valid until the thread's next failing
+ *    call).  Reference panics (infeasible config, kernarg-length mismatch,
+ *    LDS over budget) become T0MI_ERR_INVALID / T0MI_ERR_KERNARG here.
+ *  - Device pointers are uint64_t GPU virtual addresses, as in the reference's
+ *    kernarg builders (GpuBuffer::gpu_addr()).
+ *  - Argument order follows the reference function being replaced, including
+ *    its quirks: build_kernargs takes (x, wt, y, k, n, m), auto_select takes
+ *    (m, k, n), GemmTuner::tune takes (m, n, k).
+ *  - Grids are HSA work-item grids, as in the reference (grid_x = tiles * wg);
+ *    the HIP shim converts them to workgroup counts at launch.
+ */
+#ifndef T0MI_H
+#define T0MI_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define T0MI_ABI_VERSION 1
+
+/* ---- status codes ---------------------------------------------------- */
+#define T0MI_OK 0
+#define T0MI_ERR_INVALID (-1)   /* bad argument / infeasible config (reference: panic) */
+#define T0MI_ERR_NO_KERNEL (-2) /* no prebuilt gfx950 code object for this config */
+#define T0MI_ERR_HIP (-3)       /* HIP runtime failure (alloc, copy, launch) */
+#define T0MI_ERR_POISONED (-4)  /* runtime poisoned by an earlier failed wait */
+#define T0MI_ERR_KERNARG (-5)   /* kernarg length differs from the kernel's declaration */
+#define T0MI_ERR_TIMEOUT (-6)   /* dispatch did not complete in time; runtime poisoned */
+#define T0MI_ERR_NOT_FOUND (-7) /* cache miss / unknown preset */
+#define T0MI_ERR_NO_DEVICE (-8) /* no gfx950 device visible */
+
+/* Thread-local description of the last error on this thread. */
+const char* t0mi_last_error(void);
+/* ABI version and the gfx target the kernels were built for ("gfx950"). */
+int t0mi_abi_version(void);
+const char* t0mi_build_target(void);
+
+/* ---- GemmConfig (src/t0/gemm_gen.rs:22-84) ----------------------------- */
+typedef enum { T0MI_NT = 0, T0MI_NN = 1 } t0mi_transpose;            /* gemm_gen.rs:22-29 */
+typedef enum {                                                        /* gemm_gen.rs:41-49 */
+  T0MI_EPI_STORE_F32 = 0,
+  T0MI_EPI_BIAS_ADD_STORE_F32 = 1,
+  T0MI_EPI_BIAS_ADD_RELU_STORE_F32 = 2
+} t0mi_epilogue;
+typedef enum { T0MI_OUT_F32 = 0, T0MI_OUT_BF16 = 1 } t0mi_out_dtype; /* new: bf16 store, RNE */
+
+/* Field-for-field mirror of GemmConfig (gemm_gen.rs:55-84).  Booleans are
+ * uint32_t 0/1; split_k 0 or 1 means None.  The last three fields are gfx950
+ * extensions with no reference counterpart; zero keeps reference behaviour
+ * (f32 output, wave layout derived from wg_size).
+ * wg_size is the real workgroup size in threads (64-wide waves on gfx950);
+ * the reference's wave32 presets with wg_size 32 are infeasible here. */
+typedef struct t0mi_gemm_config {
+  uint32_t tile_m, tile_n, tile_k, wg_size;
+  uint32_t use_lds, double_buffer;
+  uint32_t split_k;
+  uint32_t lds_pad, n_col_passes;
+  uint32_t swap_grid, wgp_mode;
+  uint32_t transpose; /* t0mi_transpose */
+  uint32_t epilogue;  /* t0mi_epilogue */
+  uint32_t out_dtype; /* t0mi_out_dtype (gfx950 extension) */
+  uint32_t wave_m, wave_n; /* waves along M and N; 0,0 = derive (gfx950 extension) */
+} t0mi_gemm_config;
+
+/* Presets by reference name, e.g. "tile_128x64_k16" (gemm_gen.rs:87-145), plus
+ * the gfx950 presets listed by t0mi_config_preset_names().  Returns
+ * T0MI_ERR_NOT_FOUND for an unknown name. */
+int t0mi_config_preset(const char* name, t0mi_gemm_config* out);
+/* Comma-separated preset names; writes at most len bytes (NUL-terminated). */
+int t0mi_config_preset_names(char* buf, size_t len);
+/* Derived quantities (gemm_gen.rs:147-201). */
+uint32_t t0mi_config_n_waves(const t0mi_gemm_config* cfg);
+uint32_t t0mi_config_lds_total(const t0mi_gemm_config* cfg);
+uint32_t t0mi_config_estimated_regs(const t0mi_gemm_config* cfg);
+/* gemm_gen.rs:203-213, re-derived for gfx950 limits (wave64, 512 VGPR+AGPR,
+ * 160 KB LDS).  Returns 1 if feasible, 0 otherwise. */
+int t0mi_config_is_feasible(const t0mi_gemm_config* cfg);
+/* GemmConfig::name (gemm_gen.rs:215-235): same tags, plus "_bf16o" for bf16
+ * output and "_w{M}x{N}" for a non-default wave layout.  It is the kernel
+ * cache key.  Returns the full length (like snprintf). */
+int t0mi_config_name(const t0mi_gemm_config* cfg, char* buf, size_t len);
+
+/* ---- grids and kernargs (byte-identical to the Rust builders) ----------- */
+/* compute_grid / compute_grid_split_k / compute_grid_auto (gemm_gen.rs:308-329, 430-437). */
+int t0mi_compute_grid(const t0mi_gemm_config* cfg, uint32_t m, uint32_t n, uint32_t grid[2]);
+int t0mi_compute_grid_split_k(const t0mi_gemm_config* cfg, uint32_t m, uint32_t n, uint32_t split_k,
+                              uint32_t grid[2]);
+int t0mi_compute_grid_auto(const t0mi_gemm_config* cfg, uint32_t m, uint32_t n, uint32_t grid[2]);
+/* build_kernargs (gemm_gen.rs:439-458): 40 bytes
+ *   [X u64 @0, WT u64 @8, Y u64 @16, K u32 @24, N u32 @28, split_k_shift u32 @32 (=0),
+ *    y_split_stride u32 @36 (= m*n*4 if split_k > 1)]. */
+int t0mi_build_kernargs(uint64_t x, uint64_t wt, uint64_t y, uint32_t k, uint32_t n, uint32_t m,
+                        const t0mi_gemm_config* cfg, uint8_t out[40]);
+/* build_kernargs_with_bias (gemm_gen.rs:460-484): 48 bytes, bias u64 @40. */
+int t0mi_build_kernargs_with_bias(uint64_t x, uint64_t wt, uint64_t y, uint32_t k, uint32_t n,
+                                  uint32_t m, const t0mi_gemm_config* cfg, uint64_t bias,
+                                  uint8_t out[48]);
+
+/* ---- selection and tuning ---------------------------------------------- */
+/* auto_select(m, k, n) (gemm_gen.rs:340 -> cost_model::predict_best): a gfx950
+ * cost model over the prebuilt kernels.  transpose / out_dtype of the result
+ * are T0MI_NT / T0MI_OUT_F32 like the reference; callers set them after. */
+int t0mi_auto_select(uint32_t m, uint32_t k, uint32_t n, t0mi_gemm_config* out);
+/* auto_select_legacy (gemm_gen.rs:351-404), re-derived for gfx950. */
+int t0mi_auto_select_legacy(uint32_t m, uint32_t k, uint32_t n, t0mi_gemm_config* out);
+/* cached_auto_select (src/t0/prefill_spec_cache.rs:42-76): process-wide cache. */
+int t0mi_cached_auto_select(uint32_t m, uint32_t k, uint32_t n, t0mi_gemm_config* out);
+void t0mi_clear_spec_cache(void);
+size_t t0mi_spec_cache_len(void);
+
+/* ---- runtime: GpuRuntime / GpuKernel (src/ignis/gpu_context.rs, src/kfd/) - */
+typedef struct t0mi_ctx t0mi_ctx;       /* GpuRuntime (gpu_context.rs:99-120) */
+typedef struct t0mi_kernel t0mi_kernel; /* GpuKernel (src/kfd/kernel.rs) */
+
+/* GpuRuntime::new (gpu_context.rs:151): opens a HIP device (the first gfx950
+ * one when device < 0) and creates its own stream (default priority). */
+int t0mi_ctx_create(int device, t0mi_ctx** out);
+/* Same, but launches go to an existing hipStream_t owned by the caller
+ * (for example torch.cuda.current_stream().cuda_stream); NULL means the
+ * device's null (default) stream, not a new one. */
+int t0mi_ctx_create_on_stream(int device, void* hip_stream, t0mi_ctx** out);
+/* A runtime with no device: dispatches are validated (kernarg length,
+ * poisoning) and recorded but compute nothing.  For control-path tests. */
+int t0mi_ctx_create_null(t0mi_ctx** out);
+void t0mi_ctx_destroy(t0mi_ctx* ctx);
+void* t0mi_ctx_stream(t0mi_ctx* ctx);
+/* GpuRuntime::is_poisoned / mark_poisoned (gpu_context.rs:190-197). */
+int t0mi_is_poisoned(t0mi_ctx* ctx);
+void t0mi_mark_poisoned(t0mi_ctx* ctx);
+/* Timeout of a synchronous dispatch / wait (aql.rs:481-545 uses 60 s). */
+void t0mi_set_timeout_ms(t0mi_ctx* ctx, uint32_t ms);
+/* Null runtime only: make the next dispatch report a timeout. */
+int t0mi_null_inject_timeout(t0mi_ctx* ctx);
+/* Null runtime only: grid (work-items) and kernarg bytes of the last dispatch. */
+int t0mi_null_last_dispatch(t0mi_ctx* ctx, uint32_t grid[3], uint8_t* ka, size_t ka_cap, size_t* ka_len);
+
+/* GpuRuntime::alloc / alloc_zero / recycle / read_f32 / write (gpu_context.rs:508-545). */
+int t0mi_alloc(t0mi_ctx* ctx, size_t bytes, uint64_t* dptr);
+int t0mi_alloc_zero(t0mi_ctx* ctx, size_t bytes, uint64_t* dptr);
+int t0mi_free(t0mi_ctx* ctx, uint64_t dptr);
+int t0mi_h2d(t0mi_ctx* ctx, uint64_t dst, const void* src, size_t bytes);
+int t0mi_d2h(t0mi_ctx* ctx, void* dst, uint64_t src, size_t bytes);
+int t0mi_memset(t0mi_ctx* ctx, uint64_t dst, int value, size_t bytes);
+
+/* ensure_kernel_t0(cfg.name(), || generate(&cfg), ...) (gpu_context.rs:212-265):
+ * instead of generate + compile + GpuKernel::load, look up the prebuilt gfx950
+ * code object for this config (cached by name).  kernarg_size is 40, or 48 for
+ * a bias epilogue.  The kernel is owned by ctx. */
+int t0mi_kernel_get(t0mi_ctx* ctx, const t0mi_gemm_config* cfg, t0mi_kernel** out);
+/* T0Kernel::lds_size / wg_size / kernarg_size (compile.rs:641-656). */
+int t0mi_kernel_attrs(const t0mi_kernel* k, uint32_t* lds_size, uint32_t* wg_size, uint32_t* kernarg_size);
+int t0mi_kernel_name(const t0mi_kernel* k, char* buf, size_t len);
+
+/* GpuRuntime::dispatch (gpu_context.rs:305-357): checks poisoning, requires
+ * ka_len == kernarg_size (reference: assert), launches grid_workitems / wg
+ * workgroups and waits (with timeout; a timeout poisons the runtime). */
+int t0mi_dispatch(t0mi_ctx* ctx, const t0mi_kernel* k, const uint32_t grid_workitems[3],
+                  const uint8_t* ka, size_t ka_len);
+/* GpuRuntime::dispatch_async (gpu_context.rs:400-410): no wait. */
+int t0mi_dispatch_async(t0mi_ctx* ctx, const t0mi_kernel* k, const uint32_t grid_workitems[3],
+                        const uint8_t* ka, size_t ka_len);
+/* GpuRuntime::wait_idle / synchronize (gpu_context.rs:446-452). */
+int t0mi_wait_idle(t0mi_ctx* ctx);
+
+/* One-call GEMM with a given config (what callers of generate + build_kernargs
+ * + compute_grid_auto + dispatch do, src/t0/auto_gemm.rs:575-588), without the
+ * reference's padding contract: M, N, K need not be tile multiples (K, and N for
+ * NN, must be multiples of 8; rows are 16-byte aligned).  Y is [m, n] with the
+ * config's out_dtype.  Split-K > 1 is reduced in a deterministic second pass
+ * (p = 0..split_k-1 order) using a library-owned workspace.  Asynchronous. */
+int t0mi_gemm(t0mi_ctx* ctx, const t0mi_gemm_config* cfg, uint64_t x, uint64_t b, uint64_t y,
+              uint64_t bias, uint32_t m, uint32_t n, uint32_t k);
+
+/* ---- autotuner: GemmTuner (src/t0/auto_gemm.rs:46-527) -------------------- */
+typedef struct t0mi_tuner t0mi_tuner;
+/* GemmTuner::new (default cache dir $HOME/.t0mi_autotune_gfx950, kept apart
+ * from the reference's RDNA cache) / with_cache_dir. */
+int t0mi_tuner_create(const char* cache_dir_or_null, t0mi_tuner** out);
+void t0mi_tuner_destroy(t0mi_tuner* t);
+/* max_candidates (default 8) and n_iters (default 5) (auto_gemm.rs:57-65). */
+void t0mi_tuner_set_params(t0mi_tuner* t, uint32_t max_candidates, uint32_t n_iters);
+/* GemmTuner::tune(rt, m, n, k) (auto_gemm.rs:82-216): memory cache -> disk JSON
+ * -> candidates -> 256^3 smoke test -> median timing -> persist.  transpose
+ * and out_dtype select the variant being tuned.  *tflops and *from_cache may
+ * be null. */
+int t0mi_tuner_tune(t0mi_tuner* t, t0mi_ctx* ctx, uint32_t m, uint32_t n, uint32_t k, uint32_t transpose,
+                    uint32_t out_dtype, t0mi_gemm_config* best, double* tflops, int* from_cache);
+/* GemmTuner::invalidate / clear (auto_gemm.rs:504-514). */
+void t0mi_tuner_invalidate(t0mi_tuner* t, uint32_t m, uint32_t n, uint32_t k, uint32_t transpose,
+                           uint32_t out_dtype);
+void t0mi_tuner_clear(t0mi_tuner* t);
+/* Cache file path for a key (auto_gemm.rs:435-437), and its JSON codec. */
+int t0mi_tuner_cache_path(t0mi_tuner* t, uint32_t m, uint32_t n, uint32_t k, uint32_t transpose,
+                          uint32_t out_dtype, char* buf, size_t len);
+/* GemmTuner::report as text (auto_gemm.rs:517-527). */
+int t0mi_tuner_report(t0mi_tuner* t, char* buf, size_t len);
+/* auto_gemm(rt, a, b, c, m, n, k) (auto_gemm.rs:555-590) with the process-wide
+ * tuner; NT layout, f32 output as in the reference.  Returns the cached
+ * TFLOPS in *tflops. */
+int t0mi_auto_gemm(t0mi_ctx* ctx, uint64_t a, uint64_t b, uint64_t c, uint32_t m, uint32_t n, uint32_t k,
+                   double* tflops);
+
+/* ---- W4A16: INT4-dequant GEMM (new; semantics from src/t0/quant_kernels.rs) */
+/* Y[m, n] = sum_k A[m,k] * (q[k][n] - z) * s[k/group][n], fp32 accumulate.
+ *  A       bf16 [m, k] row-major.
+ *  qweight u32 [k/8][n]: 8 nibbles along K per word, nibble e = bits 4e..4e+3
+ *          (the reference's low-nibble-first element order, quant_kernels.rs:3-10).
+ *  scales  bf16 [k/group][n].
+ *  qzeros  u32 [k/group][n/8] (nibble e of word j = zero of column 8j+e), or 0
+ *          to use the constant zp_const for every group.
+ *  Y       [m, n] f32 or bf16 (RNE) per out_dtype.
+ * Requires k % group == 0, group % 32 == 0, n % 8 == 0. Asynchronous. */
+int t0mi_w4a16_gemm(t0mi_ctx* ctx, uint64_t a, uint64_t qweight, uint64_t scales, uint64_t qzeros,
+                    uint32_t zp_const, uint64_t y, uint32_t m, uint32_t k, uint32_t n, uint32_t group,
+                    uint32_t out_dtype);
+
+/* Standalone dequant, replacing build_dequant_int4_{f32,bf16} (quant_kernels.rs:53-171)
+ * on the same layouts as t0mi_w4a16_gemm: out[k][n] = (float)(q - z) * s.
+ * round_mode 0: f32 out; 1: bf16 by truncation (the reference's store_bf16,
+ * quant_kernels.rs:167-168); 2: bf16 round-to-nearest-even.  Bit-exact. */
+int t0mi_dequant_int4(t0mi_ctx* ctx, uint64_t qweight, uint64_t scales, uint64_t qzeros, uint32_t zp_const,
+                      uint64_t out, uint32_t k, uint32_t n, uint32_t group, uint32_t round_mode);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* T0MI_H */

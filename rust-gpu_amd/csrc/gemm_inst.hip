@@ -1,0 +1,33 @@
+// gemm_inst.hip — instantiates one block of gemm_variants.def for one B layout.
+// Compiled four times by the build (T0MI_PART = 0/1, T0MI_INST_NN = 0/1, with
+// T0MI_TABLE_FN naming the table accessor) so the variants build in parallel.
+#include "t0mi_ctx.h"
+
+#ifndef T0MI_PART
+#error "T0MI_PART must be defined"
+#endif
+#ifndef T0MI_INST_NN
+#error "T0MI_INST_NN must be defined"
+#endif
+
+namespace t0mi {
+
+#define T0MI_V(BM, BN, BK, WM, WN)                                                          \
+  static void launch_##BM##_##BN##_##BK##_##WM##_##WN(dim3 g, hipStream_t s, const GemmParams& p) { \
+    hipLaunchKernelGGL((gemm_bf16_kernel<BM, BN, BK, WM, WN, (T0MI_INST_NN != 0)>), g, dim3(WM * WN * 64), 0, s, p); \
+  }
+#include "gemm_variants.def"
+#undef T0MI_V
+
+static const GemmLaunchEntry kTable[] = {
+#define T0MI_V(BM, BN, BK, WM, WN) {BM, BN, BK, WM, WN, T0MI_INST_NN, launch_##BM##_##BN##_##BK##_##WM##_##WN},
+#include "gemm_variants.def"
+#undef T0MI_V
+};
+
+const GemmLaunchEntry* T0MI_TABLE_FN(size_t* n) {
+  *n = sizeof kTable / sizeof kTable[0];
+  return kTable;
+}
+
+}  // namespace t0mi

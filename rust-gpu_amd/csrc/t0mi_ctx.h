@@ -1,0 +1,71 @@
+// t0mi_ctx.h — runtime object shared by the libt0mi translation units.
+#pragma once
+#include <hip/hip_runtime.h>
+
+#include <atomic>
+#include <map>
+#include <memory>
+#include <mutex>
+#include <string>
+#include <vector>
+
+#include "gemm_bf16_kernel.h"
+#include "t0mi_internal.h"
+
+namespace t0mi {
+
+typedef void (*GemmLaunchFn)(dim3 grid, hipStream_t stream, const GemmParams& p);
+struct GemmLaunchEntry {
+  int bm, bn, bk, wm, wn, nn;
+  GemmLaunchFn fn;
+};
+// Tables defined by the gemm_inst.hip objects (one per variant block and layout).
+const GemmLaunchEntry* gemm_table_p0_nt(size_t* n);
+const GemmLaunchEntry* gemm_table_p1_nt(size_t* n);
+const GemmLaunchEntry* gemm_table_p0_nn(size_t* n);
+const GemmLaunchEntry* gemm_table_p1_nn(size_t* n);
+const GemmLaunchEntry* find_gemm_launch(const t0mi_gemm_config& c);
+
+enum KernelKind : int { KK_GEMM_GEN = 1 };
+
+}  // namespace t0mi
+
+struct t0mi_kernel {
+  int kind;
+  t0mi_gemm_config cfg;
+  std::string name;
+  uint32_t kernarg_size, lds_size, wg_size;
+  const t0mi::GemmLaunchEntry* gemm;
+};
+
+struct t0mi_ctx {
+  bool null_backend = false;
+  int device = -1;
+  hipStream_t stream = nullptr;
+  bool own_stream = false;
+  std::atomic<bool> poisoned{false};
+  uint32_t timeout_ms = 60000;  // aql.rs:481-545: 60 s
+  std::mutex mu;
+  std::map<std::string, std::unique_ptr<t0mi_kernel>> kernels;  // name -> kernel (ensure_kernel_t0 cache)
+  std::map<uint64_t, size_t> allocs;                            // live t0mi_alloc buffers
+  // Library-owned workspace (split-K partial planes, W4A16 partials).
+  void* ws = nullptr;
+  size_t ws_bytes = 0;
+  // Null backend: injected failure and the last recorded dispatch.
+  bool inject_timeout = false;
+  uint32_t last_grid[3] = {0, 0, 0};
+  std::vector<uint8_t> last_ka;
+  int cu_count = 256;
+};
+
+namespace t0mi {
+// Grows ctx->ws to at least `bytes` (waits for the stream first).
+int ensure_workspace(t0mi_ctx* ctx, size_t bytes);
+// Launches the bf16 GEMM kernel for (cfg, params) on ctx's stream.
+int launch_gemm(t0mi_ctx* ctx, const t0mi_gemm_config& cfg, const GemmLaunchEntry* e, GemmParams p);
+int check_ctx(t0mi_ctx* ctx);
+// Sums sk f32 planes of [M, N] (ascending plane order), applies the epilogue
+// and stores f32 or bf16 into y (row stride ldy), on ctx's stream.
+int launch_splitk_reduce(t0mi_ctx* ctx, const float* ws, void* y, const float* bias, uint32_t M, uint32_t N,
+                         uint32_t ldy, uint32_t sk, uint32_t out_bf16, uint32_t epilogue);
+}  // namespace t0mi

@@ -1,0 +1,522 @@
+// t0mi_runtime.hip — the HIP shim that replaces the reference's KFD/AQL runtime.
+//
+//   GpuRuntime::new / dispatch / dispatch_async / wait_idle / alloc / poison
+//       src/ignis/gpu_context.rs:151-545
+//   GpuKernel::load + KernelLoadConfig            src/kfd/kernel.rs:26-141
+//   AqlQueue::submit / synchronize (timeout)      src/kfd/aql.rs:184-249, 481-545
+//
+// Kernels are not generated and assembled at run time: every config maps to a
+// prebuilt gfx950 kernel in this library (gemm_inst.hip).  Dispatch keeps the
+// reference's contract — HSA work-item grids, raw kernarg bytes whose length
+// must equal the kernel's declaration, synchronous wait with a timeout that
+// poisons the runtime — and turns it into a hipLaunchKernelGGL on the
+// runtime's stream.
+#include <string.h>
+#include <time.h>
+
+#include "t0mi_ctx.h"
+
+using namespace t0mi;
+
+namespace t0mi {
+
+const GemmLaunchEntry* find_gemm_launch(const t0mi_gemm_config& c) {
+  uint32_t wm, wn;
+  if (!wave_layout(c, &wm, &wn)) return nullptr;
+  const bool nn = c.transpose == T0MI_NN;
+  const GemmLaunchEntry* (*tables[])(size_t*) = {nn ? gemm_table_p0_nn : gemm_table_p0_nt,
+                                                nn ? gemm_table_p1_nn : gemm_table_p1_nt};
+  for (auto tf : tables) {
+    size_t n = 0;
+    const GemmLaunchEntry* t = tf(&n);
+    for (size_t i = 0; i < n; ++i)
+      if ((uint32_t)t[i].bm == c.tile_m && (uint32_t)t[i].bn == c.tile_n && (uint32_t)t[i].bk == c.tile_k &&
+          (uint32_t)t[i].wm == wm && (uint32_t)t[i].wn == wn)
+        return &t[i];
+  }
+  return nullptr;
+}
+
+int check_ctx(t0mi_ctx* ctx) {
+  if (!ctx) return set_error(T0MI_ERR_INVALID, "null runtime");
+  if (ctx->poisoned.load())
+    return set_error(T0MI_ERR_POISONED,
+                     "[t0mi] runtime poisoned after a failed wait; refusing dispatch (create a new runtime)");
+  return T0MI_OK;
+}
+
+static int hip_fail(hipError_t e, const char* what) {
+  return set_error(T0MI_ERR_HIP, "%s: %s", what, hipGetErrorString(e));
+}
+
+int ensure_workspace(t0mi_ctx* ctx, size_t bytes) {
+  if (ctx->ws_bytes >= bytes) return T0MI_OK;
+  if (ctx->null_backend) {
+    ctx->ws_bytes = bytes;
+    return T0MI_OK;
+  }
+  hipError_t e = hipStreamSynchronize(ctx->stream);
+  if (e != hipSuccess) return hip_fail(e, "hipStreamSynchronize");
+  if (ctx->ws) (void)hipFree(ctx->ws);
+  ctx->ws = nullptr;
+  ctx->ws_bytes = 0;
+  size_t want = bytes + (bytes >> 2);  // grow with slack
+  e = hipMalloc(&ctx->ws, want);
+  if (e != hipSuccess) return hip_fail(e, "hipMalloc(workspace)");
+  ctx->ws_bytes = want;
+  return T0MI_OK;
+}
+
+int launch_gemm(t0mi_ctx* ctx, const t0mi_gemm_config& cfg, const GemmLaunchEntry* e, GemmParams p) {
+  const uint32_t nwg = p.tiles_m * p.tiles_n * p.split_k;
+  if (nwg == 0) return T0MI_OK;
+  // Grid axes follow the reference convention (swap_grid: x -> N tiles); the
+  // kernel decodes the tile from the linear workgroup id either way.
+  dim3 grid = cfg.swap_grid ? dim3(p.tiles_n, p.tiles_m * p.split_k) : dim3(p.tiles_m, p.tiles_n * p.split_k);
+  p.swap_grid = cfg.swap_grid;
+  if (ctx->null_backend) return T0MI_OK;
+  e->fn(grid, ctx->stream, p);
+  hipError_t err = hipGetLastError();
+  if (err != hipSuccess) return hip_fail(err, "gemm launch");
+  return T0MI_OK;
+}
+
+}  // namespace t0mi
+
+// ------------------------------------------------------------ split-K reduce --
+// Deterministic reduction of split-K partial planes: y = sum_{p=0..sk-1} ws[p]
+// in ascending p, then bias / ReLU, then f32 or bf16 (RNE) store.
+__global__ __launch_bounds__(256) void t0mi_splitk_reduce(const float* __restrict__ ws, void* __restrict__ y,
+                                                          const float* __restrict__ bias, uint32_t M, uint32_t N,
+                                                          uint32_t ldy, uint32_t sk, uint32_t out_bf16,
+                                                          uint32_t epilogue) {
+  const size_t plane = (size_t)M * N;
+  const size_t nvec = plane / 4;
+  for (size_t v = blockIdx.x * (size_t)blockDim.x + threadIdx.x; v < nvec; v += (size_t)gridDim.x * blockDim.x) {
+    const size_t idx = v * 4;
+    const uint32_t m = (uint32_t)(idx / N), n = (uint32_t)(idx % N);
+    f32x4 s = *(const f32x4*)(ws + idx);
+    for (uint32_t q = 1; q < sk; ++q) {
+      const f32x4 t = *(const f32x4*)(ws + q * plane + idx);
+      s.x += t.x;
+      s.y += t.y;
+      s.z += t.z;
+      s.w += t.w;
+    }
+    if (epilogue != EPI_NONE) {
+      s.x += bias[n];
+      s.y += bias[n + 1];
+      s.z += bias[n + 2];
+      s.w += bias[n + 3];
+      if (epilogue == EPI_BIAS_RELU) {
+        s.x = fmaxf(s.x, 0.f);
+        s.y = fmaxf(s.y, 0.f);
+        s.z = fmaxf(s.z, 0.f);
+        s.w = fmaxf(s.w, 0.f);
+      }
+    }
+    if (out_bf16) {
+      u32x2 o;
+      o.x = (uint32_t)f32_to_bf16_rne(s.x) | ((uint32_t)f32_to_bf16_rne(s.y) << 16);
+      o.y = (uint32_t)f32_to_bf16_rne(s.z) | ((uint32_t)f32_to_bf16_rne(s.w) << 16);
+      *(u32x2*)((uint16_t*)y + (size_t)m * ldy + n) = o;
+    } else {
+      *(f32x4*)((float*)y + (size_t)m * ldy + n) = s;
+    }
+  }
+}
+
+namespace t0mi {
+int launch_splitk_reduce(t0mi_ctx* ctx, const float* ws, void* y, const float* bias, uint32_t M, uint32_t N,
+                         uint32_t ldy, uint32_t sk, uint32_t out_bf16, uint32_t epilogue) {
+  if (ctx->null_backend) return T0MI_OK;
+  const size_t nvec = (size_t)M * N / 4;
+  if (nvec == 0) return T0MI_OK;
+  const uint32_t blocks = (uint32_t)std::min<size_t>((nvec + 255) / 256, (size_t)ctx->cu_count * 8);
+  hipLaunchKernelGGL(t0mi_splitk_reduce, dim3(blocks), dim3(256), 0, ctx->stream, ws, y, bias, M, N, ldy, sk,
+                     out_bf16, epilogue);
+  hipError_t e = hipGetLastError();
+  return e == hipSuccess ? T0MI_OK : hip_fail(e, "reduce launch");
+}
+}  // namespace t0mi
+
+// ===================================================================== C ABI ==
+
+static int ctx_create(int device, bool use_given_stream, void* hip_stream, t0mi_ctx** out) {
+  if (!out) return set_error(T0MI_ERR_INVALID, "null out");
+  *out = nullptr;
+  int n = 0;
+  hipError_t e = hipGetDeviceCount(&n);
+  if (e != hipSuccess || n == 0) return set_error(T0MI_ERR_NO_DEVICE, "no HIP device visible (%s)", hipGetErrorString(e));
+  int dev = device;
+  if (dev < 0) {
+    for (int i = 0; i < n; ++i) {
+      hipDeviceProp_t pr;
+      if (hipGetDeviceProperties(&pr, i) == hipSuccess && strncmp(pr.gcnArchName, "gfx950", 6) == 0) {
+        dev = i;
+        break;
+      }
+    }
+    if (dev < 0) return set_error(T0MI_ERR_NO_DEVICE, "no gfx950 device among %d HIP devices", n);
+  }
+  if (dev >= n) return set_error(T0MI_ERR_NO_DEVICE, "device %d out of range (%d devices)", dev, n);
+  hipDeviceProp_t pr;
+  e = hipGetDeviceProperties(&pr, dev);
+  if (e != hipSuccess) return hip_fail(e, "hipGetDeviceProperties");
+  if (strncmp(pr.gcnArchName, "gfx950", 6) != 0)
+    return set_error(T0MI_ERR_NO_DEVICE, "device %d is %s; kernels are built for gfx950 only", dev, pr.gcnArchName);
+  e = hipSetDevice(dev);
+  if (e != hipSuccess) return hip_fail(e, "hipSetDevice");
+  t0mi_ctx* c = new t0mi_ctx();
+  c->device = dev;
+  c->cu_count = pr.multiProcessorCount;
+  if (use_given_stream) {
+    // The caller's stream, including the null (default) stream.
+    c->stream = (hipStream_t)hip_stream;
+    c->own_stream = false;
+  } else {
+    e = hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking);
+    if (e != hipSuccess) {
+      delete c;
+      return hip_fail(e, "hipStreamCreate");
+    }
+    c->own_stream = true;
+  }
+  *out = c;
+  return T0MI_OK;
+}
+
+extern "C" int t0mi_ctx_create_on_stream(int device, void* hip_stream, t0mi_ctx** out) {
+  return ctx_create(device, true, hip_stream, out);
+}
+
+extern "C" int t0mi_ctx_create(int device, t0mi_ctx** out) { return ctx_create(device, false, nullptr, out); }
+
+extern "C" int t0mi_ctx_create_null(t0mi_ctx** out) {
+  if (!out) return set_error(T0MI_ERR_INVALID, "null out");
+  t0mi_ctx* c = new t0mi_ctx();
+  c->null_backend = true;
+  *out = c;
+  return T0MI_OK;
+}
+
+extern "C" void t0mi_ctx_destroy(t0mi_ctx* ctx) {
+  if (!ctx) return;
+  if (!ctx->null_backend) {
+    (void)hipSetDevice(ctx->device);
+    if (!ctx->poisoned.load()) (void)hipStreamSynchronize(ctx->stream);
+    for (auto& kv : ctx->allocs) (void)hipFree((void*)kv.first);
+    if (ctx->ws) (void)hipFree(ctx->ws);
+    if (ctx->own_stream) (void)hipStreamDestroy(ctx->stream);
+  }
+  delete ctx;
+}
+
+extern "C" void* t0mi_ctx_stream(t0mi_ctx* ctx) { return ctx ? (void*)ctx->stream : nullptr; }
+extern "C" int t0mi_is_poisoned(t0mi_ctx* ctx) { return ctx && ctx->poisoned.load() ? 1 : 0; }
+extern "C" void t0mi_mark_poisoned(t0mi_ctx* ctx) {
+  if (ctx) ctx->poisoned.store(true);
+}
+extern "C" void t0mi_set_timeout_ms(t0mi_ctx* ctx, uint32_t ms) {
+  if (ctx) ctx->timeout_ms = ms;
+}
+
+extern "C" int t0mi_null_inject_timeout(t0mi_ctx* ctx) {
+  if (!ctx || !ctx->null_backend) return set_error(T0MI_ERR_INVALID, "not a null runtime");
+  ctx->inject_timeout = true;
+  return T0MI_OK;
+}
+
+extern "C" int t0mi_null_last_dispatch(t0mi_ctx* ctx, uint32_t grid[3], uint8_t* ka, size_t ka_cap, size_t* ka_len) {
+  if (!ctx || !ctx->null_backend) return set_error(T0MI_ERR_INVALID, "not a null runtime");
+  if (grid) memcpy(grid, ctx->last_grid, sizeof ctx->last_grid);
+  if (ka_len) *ka_len = ctx->last_ka.size();
+  if (ka && ka_cap) memcpy(ka, ctx->last_ka.data(), std::min(ka_cap, ctx->last_ka.size()));
+  return T0MI_OK;
+}
+
+// ---------------------------------------------------------------- memory ----
+
+extern "C" int t0mi_alloc(t0mi_ctx* ctx, size_t bytes, uint64_t* dptr) {
+  if (!ctx || !dptr) return set_error(T0MI_ERR_INVALID, "null argument");
+  if (ctx->null_backend) return set_error(T0MI_ERR_NO_DEVICE, "null runtime has no memory");
+  void* p = nullptr;
+  hipError_t e = hipMalloc(&p, bytes ? bytes : 1);
+  if (e != hipSuccess) return hip_fail(e, "hipMalloc");
+  std::lock_guard<std::mutex> lk(ctx->mu);
+  ctx->allocs[(uint64_t)p] = bytes;
+  *dptr = (uint64_t)p;
+  return T0MI_OK;
+}
+
+extern "C" int t0mi_alloc_zero(t0mi_ctx* ctx, size_t bytes, uint64_t* dptr) {
+  int rc = t0mi_alloc(ctx, bytes, dptr);
+  if (rc) return rc;
+  hipError_t e = hipMemsetAsync((void*)*dptr, 0, bytes, ctx->stream);
+  if (e == hipSuccess) e = hipStreamSynchronize(ctx->stream);
+  return e == hipSuccess ? T0MI_OK : hip_fail(e, "hipMemset");
+}
+
+extern "C" int t0mi_free(t0mi_ctx* ctx, uint64_t dptr) {
+  if (!ctx) return set_error(T0MI_ERR_INVALID, "null runtime");
+  std::lock_guard<std::mutex> lk(ctx->mu);
+  auto it = ctx->allocs.find(dptr);
+  if (it == ctx->allocs.end()) return set_error(T0MI_ERR_INVALID, "pointer 0x%llx was not allocated by t0mi_alloc", (unsigned long long)dptr);
+  (void)hipStreamSynchronize(ctx->stream);
+  hipError_t e = hipFree((void*)dptr);
+  ctx->allocs.erase(it);
+  return e == hipSuccess ? T0MI_OK : hip_fail(e, "hipFree");
+}
+
+extern "C" int t0mi_h2d(t0mi_ctx* ctx, uint64_t dst, const void* src, size_t bytes) {
+  if (!ctx || ctx->null_backend) return set_error(T0MI_ERR_INVALID, "no device runtime");
+  hipError_t e = hipMemcpyAsync((void*)dst, src, bytes, hipMemcpyHostToDevice, ctx->stream);
+  if (e == hipSuccess) e = hipStreamSynchronize(ctx->stream);
+  return e == hipSuccess ? T0MI_OK : hip_fail(e, "hipMemcpy H2D");
+}
+
+extern "C" int t0mi_d2h(t0mi_ctx* ctx, void* dst, uint64_t src, size_t bytes) {
+  if (!ctx || ctx->null_backend) return set_error(T0MI_ERR_INVALID, "no device runtime");
+  hipError_t e = hipMemcpyAsync(dst, (const void*)src, bytes, hipMemcpyDeviceToHost, ctx->stream);
+  if (e == hipSuccess) e = hipStreamSynchronize(ctx->stream);
+  return e == hipSuccess ? T0MI_OK : hip_fail(e, "hipMemcpy D2H");
+}
+
+extern "C" int t0mi_memset(t0mi_ctx* ctx, uint64_t dst, int value, size_t bytes) {
+  if (!ctx || ctx->null_backend) return set_error(T0MI_ERR_INVALID, "no device runtime");
+  hipError_t e = hipMemsetAsync((void*)dst, value, bytes, ctx->stream);
+  return e == hipSuccess ? T0MI_OK : hip_fail(e, "hipMemsetAsync");
+}
+
+// --------------------------------------------------------------- kernels ----
+
+extern "C" int t0mi_kernel_get(t0mi_ctx* ctx, const t0mi_gemm_config* cfg, t0mi_kernel** out) {
+  if (!ctx || !cfg || !out) return set_error(T0MI_ERR_INVALID, "null argument");
+  std::string why;
+  if (!config_feasible(*cfg, &why))
+    return set_error(T0MI_ERR_INVALID, "[t0mi] config '%s' infeasible on gfx950: %s", config_name(*cfg).c_str(),
+                     why.c_str());
+  const std::string name = config_name(*cfg);
+  std::lock_guard<std::mutex> lk(ctx->mu);
+  auto it = ctx->kernels.find(name);
+  if (it != ctx->kernels.end()) {
+    *out = it->second.get();
+    return T0MI_OK;
+  }
+  const GemmLaunchEntry* e = find_gemm_launch(*cfg);
+  if (!e) return set_error(T0MI_ERR_NO_KERNEL, "[t0mi] no prebuilt gfx950 kernel for '%s'", name.c_str());
+  std::unique_ptr<t0mi_kernel> k(new t0mi_kernel());
+  k->kind = KK_GEMM_GEN;
+  k->cfg = *cfg;
+  k->name = name;
+  k->kernarg_size = cfg->epilogue == T0MI_EPI_STORE_F32 ? 40u : 48u;
+  k->lds_size = 2u * (cfg->tile_m + cfg->tile_n) * cfg->tile_k * 2u;
+  k->wg_size = cfg->wg_size;
+  k->gemm = e;
+  *out = k.get();
+  ctx->kernels[name] = std::move(k);
+  return T0MI_OK;
+}
+
+extern "C" int t0mi_kernel_attrs(const t0mi_kernel* k, uint32_t* lds_size, uint32_t* wg_size, uint32_t* kernarg_size) {
+  if (!k) return set_error(T0MI_ERR_INVALID, "null kernel");
+  if (lds_size) *lds_size = k->lds_size;
+  if (wg_size) *wg_size = k->wg_size;
+  if (kernarg_size) *kernarg_size = k->kernarg_size;
+  return T0MI_OK;
+}
+
+extern "C" int t0mi_kernel_name(const t0mi_kernel* k, char* buf, size_t len) {
+  if (!k) return set_error(T0MI_ERR_INVALID, "null kernel");
+  if (buf && len) {
+    strncpy(buf, k->name.c_str(), len - 1);
+    buf[len - 1] = 0;
+  }
+  return (int)k->name.size();
+}
+
+static uint64_t rd_u64(const uint8_t* p) {
+  uint64_t v = 0;
+  for (int i = 7; i >= 0; --i) v = (v << 8) | p[i];
+  return v;
+}
+static uint32_t rd_u32(const uint8_t* p) { return (uint32_t)p[0] | (uint32_t)p[1] << 8 | (uint32_t)p[2] << 16 | (uint32_t)p[3] << 24; }
+
+static int wait_stream(t0mi_ctx* ctx) {
+  // AqlQueue::synchronize (aql.rs:481-545): poll completion with a timeout;
+  // a timeout poisons the runtime (gpu_context.rs:352-355).
+  if (ctx->null_backend) {
+    if (ctx->inject_timeout) {
+      ctx->inject_timeout = false;
+      ctx->poisoned.store(true);
+      return set_error(T0MI_ERR_TIMEOUT, "[t0mi] dispatch timed out after %u ms; runtime poisoned", ctx->timeout_ms);
+    }
+    return T0MI_OK;
+  }
+  hipEvent_t ev;
+  hipError_t e = hipEventCreateWithFlags(&ev, hipEventDisableTiming);
+  if (e != hipSuccess) return hip_fail(e, "hipEventCreate");
+  e = hipEventRecord(ev, ctx->stream);
+  if (e != hipSuccess) {
+    (void)hipEventDestroy(ev);
+    return hip_fail(e, "hipEventRecord");
+  }
+  struct timespec t0, t1;
+  clock_gettime(CLOCK_MONOTONIC, &t0);
+  int rc = T0MI_OK;
+  for (;;) {
+    e = hipEventQuery(ev);
+    if (e == hipSuccess) break;
+    if (e != hipErrorNotReady) {
+      ctx->poisoned.store(true);
+      rc = hip_fail(e, "dispatch failed; runtime poisoned");
+      break;
+    }
+    clock_gettime(CLOCK_MONOTONIC, &t1);
+    const double ms = (t1.tv_sec - t0.tv_sec) * 1e3 + (t1.tv_nsec - t0.tv_nsec) * 1e-6;
+    if (ms > ctx->timeout_ms) {
+      ctx->poisoned.store(true);
+      rc = set_error(T0MI_ERR_TIMEOUT, "[t0mi] dispatch timed out after %u ms; runtime poisoned", ctx->timeout_ms);
+      break;
+    }
+    struct timespec sl = {0, 10000};  // 10 us, as aql.rs:486
+    nanosleep(&sl, nullptr);
+  }
+  if (rc == T0MI_OK) (void)hipEventDestroy(ev);  // a timed-out event is leaked on purpose
+  return rc;
+}
+
+static int dispatch_impl(t0mi_ctx* ctx, const t0mi_kernel* k, const uint32_t grid[3], const uint8_t* ka,
+                         size_t ka_len) {
+  int rc = check_ctx(ctx);
+  if (rc) return rc;
+  if (!k || !grid || (!ka && ka_len)) return set_error(T0MI_ERR_INVALID, "null argument");
+  // gpu_context.rs:319-323: builder and kernel declaration must agree.
+  if (ka_len != k->kernarg_size)
+    return set_error(T0MI_ERR_KERNARG,
+                     "[t0mi] kernarg mismatch: builder produced %zuB, kernel '%s' declares %uB", ka_len,
+                     k->name.c_str(), k->kernarg_size);
+  if (grid[0] % k->wg_size)
+    return set_error(T0MI_ERR_INVALID, "grid_x=%u is not a multiple of wg_size=%u", grid[0], k->wg_size);
+  if (ctx->null_backend) {
+    memcpy(ctx->last_grid, grid, sizeof ctx->last_grid);
+    ctx->last_ka.assign(ka, ka + ka_len);
+  }
+  const t0mi_gemm_config& c = k->cfg;
+  const uint32_t sk = split_k_of(c);
+  const uint32_t gx = grid[0] / k->wg_size, gy = grid[1] ? grid[1] : 1;
+  if (gy % sk) return set_error(T0MI_ERR_INVALID, "grid_y=%u not a multiple of split_k=%u", gy, sk);
+  GemmParams p;
+  memset(&p, 0, sizeof p);
+  p.a = (const uint16_t*)rd_u64(ka + 0);
+  p.b = (const uint16_t*)rd_u64(ka + 8);
+  p.y = (void*)rd_u64(ka + 16);
+  p.K = rd_u32(ka + 24);
+  p.N = rd_u32(ka + 28);
+  p.y_split_stride = rd_u32(ka + 36);
+  p.bias = ka_len >= 48 ? (const float*)rd_u64(ka + 40) : nullptr;
+  p.tiles_n = c.swap_grid ? gx : gy / sk;
+  p.tiles_m = c.swap_grid ? gy / sk : gx;
+  // gemm_gen kernargs carry no M: the grid defines it, and callers pad Y to
+  // tiles_m * tile_m rows (gemm_gen.rs:299-307).
+  p.M = p.tiles_m * c.tile_m;
+  p.lda = p.K;
+  p.ldb = c.transpose == T0MI_NN ? p.N : p.K;
+  p.ldy = p.N;
+  p.split_k = sk;
+  p.k_per_split = sk > 1 ? p.K / sk : p.K;  // K >> split_k_shift (gemm_gen.rs:769-775)
+  p.out_bf16 = c.out_dtype == T0MI_OUT_BF16;
+  p.epilogue = c.epilogue;
+  p.xcd_remap = 1;
+  if (p.K % 8 || p.N % 8 || p.k_per_split % 8)
+    return set_error(T0MI_ERR_INVALID, "K=%u and N=%u (and K/split_k) must be multiples of 8", p.K, p.N);
+  if (p.epilogue != EPI_NONE && !p.bias) return set_error(T0MI_ERR_INVALID, "bias epilogue with null bias");
+  if (sk > 1 && p.y_split_stride < (uint64_t)p.M * p.N * 4u)
+    return set_error(T0MI_ERR_INVALID, "y_split_stride %llu smaller than an f32 plane", (unsigned long long)p.y_split_stride);
+  return launch_gemm(ctx, c, k->gemm, p);
+}
+
+extern "C" int t0mi_dispatch_async(t0mi_ctx* ctx, const t0mi_kernel* k, const uint32_t grid[3], const uint8_t* ka,
+                                   size_t ka_len) {
+  return dispatch_impl(ctx, k, grid, ka, ka_len);
+}
+
+extern "C" int t0mi_dispatch(t0mi_ctx* ctx, const t0mi_kernel* k, const uint32_t grid[3], const uint8_t* ka,
+                             size_t ka_len) {
+  int rc = dispatch_impl(ctx, k, grid, ka, ka_len);
+  if (rc) return rc;
+  return wait_stream(ctx);
+}
+
+extern "C" int t0mi_wait_idle(t0mi_ctx* ctx) {
+  if (!ctx) return set_error(T0MI_ERR_INVALID, "null runtime");
+  if (ctx->poisoned.load()) return set_error(T0MI_ERR_POISONED, "[t0mi] runtime poisoned");
+  return wait_stream(ctx);
+}
+
+// ---------------------------------------------------------- one-call GEMM ----
+
+extern "C" int t0mi_gemm(t0mi_ctx* ctx, const t0mi_gemm_config* cfg, uint64_t x, uint64_t b, uint64_t y,
+                         uint64_t bias, uint32_t m, uint32_t n, uint32_t k) {
+  int rc = check_ctx(ctx);
+  if (rc) return rc;
+  if (!cfg) return set_error(T0MI_ERR_INVALID, "null config");
+  std::string why;
+  if (!config_feasible(*cfg, &why))
+    return set_error(T0MI_ERR_INVALID, "[t0mi] config '%s' infeasible on gfx950: %s", config_name(*cfg).c_str(),
+                     why.c_str());
+  const GemmLaunchEntry* e = find_gemm_launch(*cfg);
+  if (!e) return set_error(T0MI_ERR_NO_KERNEL, "[t0mi] no prebuilt gfx950 kernel for '%s'", config_name(*cfg).c_str());
+  if (m == 0 || n == 0) return T0MI_OK;
+  if (k % 8) return set_error(T0MI_ERR_INVALID, "K=%u must be a multiple of 8", k);
+  if (n % 8) return set_error(T0MI_ERR_INVALID, "N=%u must be a multiple of 8", n);
+  if ((x | b | y) & 15) return set_error(T0MI_ERR_INVALID, "X, B and Y must be 16-byte aligned");
+  if (cfg->epilogue != T0MI_EPI_STORE_F32 && !bias) return set_error(T0MI_ERR_INVALID, "bias epilogue with null bias");
+  const uint32_t sk = split_k_of(*cfg);
+  GemmParams p;
+  memset(&p, 0, sizeof p);
+  p.a = (const uint16_t*)x;
+  p.b = (const uint16_t*)b;
+  p.bias = (const float*)bias;
+  p.M = m;
+  p.N = n;
+  p.K = k;
+  p.lda = k;
+  p.ldb = cfg->transpose == T0MI_NN ? n : k;
+  p.ldy = n;
+  p.tiles_m = (m + cfg->tile_m - 1) / cfg->tile_m;
+  p.tiles_n = (n + cfg->tile_n - 1) / cfg->tile_n;
+  p.split_k = sk;
+  p.epilogue = cfg->epilogue;
+  p.out_bf16 = cfg->out_dtype == T0MI_OUT_BF16;
+  p.xcd_remap = 1;
+  if (k == 0) {
+    // Empty contraction: the sum is zero (plus epilogue).
+    if (ctx->null_backend) return T0MI_OK;
+    rc = ensure_workspace(ctx, (size_t)m * n * 4);
+    if (rc) return rc;
+    hipError_t he = hipMemsetAsync(ctx->ws, 0, (size_t)m * n * 4, ctx->stream);
+    if (he != hipSuccess) return hip_fail(he, "hipMemsetAsync");
+    return launch_splitk_reduce(ctx, (const float*)ctx->ws, (void*)y, (const float*)bias, m, n, n, 1u, p.out_bf16,
+                                p.epilogue);
+  }
+  if (sk == 1) {
+    p.k_per_split = k;
+    p.y = (void*)y;
+    return launch_gemm(ctx, *cfg, e, p);
+  }
+  // Split-K: partitions of whole K tiles write f32 planes into the workspace,
+  // then a reduce pass sums them in partition order.
+  const uint32_t kt = (k + cfg->tile_k - 1) / cfg->tile_k;
+  p.k_per_split = ((kt + sk - 1) / sk) * cfg->tile_k;
+  const size_t plane = (size_t)m * n * 4;
+  rc = ensure_workspace(ctx, plane * sk);
+  if (rc) return rc;
+  p.y = ctx->ws;
+  p.ldy = n;
+  p.y_split_stride = plane;
+  rc = launch_gemm(ctx, *cfg, e, p);
+  if (rc || ctx->null_backend) return rc;
+  return launch_splitk_reduce(ctx, (const float*)ctx->ws, (void*)y, (const float*)bias, m, n, n, sk, p.out_bf16,
+                              p.epilogue);
+}

@@ -1,0 +1,306 @@
+// w4a16.hip — INT4-weight / bf16-activation GEMM and the standalone INT4 dequant.
+//
+// Semantics follow the reference's INT4 definition (src/t0/quant_kernels.rs:1-25,
+// 74-100): element 2i of a byte is its low nibble, w = (q - zp) * scale with
+// one scale / zero-point per group of `group` consecutive K elements.  The
+// reference has no fused W4A16 GEMM (only a standalone dequant kernel whose GPU
+// code is defective); this file is the fused gfx950 path.
+//
+// Weight layout (qweight): u32 [K/8][N]; word (kk, n) holds q[8kk+e][n] in bits
+// 4e..4e+3.  One word is exactly the 8 K-values one MFMA lane feeds for one
+// column, so the weights cross HBM once, at 4 bits, with 16-byte loads
+// (4 adjacent columns per lane).
+//
+// Dequant inside the K loop, exactly:
+//   (0x43004300 | (w >> 4j) & 0x000F000F) is the bf16 pair (128+q_j, 128+q_{j+4}),
+//   exact integers.  The MFMA multiplies them with bf16 activations in fp32
+//   (exact products), so per group and column
+//       P = sum_k a_k * (128 + q_k),   S = sum_k a_k   (S from an MFMA with ones)
+//       y += s * (P - (128 + z) * S)                      == sum_k a_k * (q_k - z) * s
+//   The activation operand is permuted to the same k order as the nibble pairs.
+#include <string.h>
+
+#include "t0mi_ctx.h"
+
+using namespace t0mi;
+
+namespace t0mi {
+
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+
+struct W4Params {
+  const uint16_t* a;       // [M, K] bf16
+  const uint32_t* w;       // [K/8, N] packed int4
+  const uint16_t* scales;  // [K/g, N] bf16
+  const uint32_t* zeros;   // [K/g, N/8] packed int4, or null -> zp_const
+  void* y;                 // [M, N] out (or f32 partial planes)
+  uint32_t M, K, N, group; // group % 32 == 0
+  uint32_t zp_const;
+  uint32_t out_bf16;
+  uint32_t kb_per_split;   // k-blocks (of 32) per grid.y partition
+  uint64_t y_split_stride; // bytes between partial planes when gridDim.y > 1
+};
+
+__device__ __forceinline__ bf16x8_t nib_pairs(uint32_t w) {
+  // 8 nibbles -> bf16 (128+q) in element order q0,q4,q1,q5,q2,q6,q3,q7.
+  u32x4 d;
+  d.x = (w & 0x000F000Fu) | 0x43004300u;
+  d.y = ((w >> 4) & 0x000F000Fu) | 0x43004300u;
+  d.z = ((w >> 8) & 0x000F000Fu) | 0x43004300u;
+  d.w = ((w >> 12) & 0x000F000Fu) | 0x43004300u;
+  return __builtin_bit_cast(bf16x8_t, d);
+}
+
+__device__ __forceinline__ bf16x8_t perm_act(u32x4 a) {
+  // a = (a0,a1)(a2,a3)(a4,a5)(a6,a7) -> (a0,a4)(a1,a5)(a2,a6)(a3,a7)
+  u32x4 o;
+  o.x = __builtin_amdgcn_perm(a.z, a.x, 0x05040100u);
+  o.y = __builtin_amdgcn_perm(a.z, a.x, 0x07060302u);
+  o.z = __builtin_amdgcn_perm(a.w, a.y, 0x05040100u);
+  o.w = __builtin_amdgcn_perm(a.w, a.y, 0x07060302u);
+  return __builtin_bit_cast(bf16x8_t, o);
+}
+
+__device__ __forceinline__ float bf16f(uint32_t h) { return __builtin_bit_cast(float, h << 16); }
+
+// Decode kernel: M <= 16 rows per slab.  One workgroup = WAVES waves on one
+// 64-column strip; wave v takes k-blocks [kb0 + v*KBW, +KBW) of this grid.y
+// partition.  Each lane issues all its 16-byte weight and activation loads up
+// front (KBW of each), then runs 4 MFMAs per k-block (one per column word).
+// Waves are reduced through LDS in wave order; with gridDim.y > 1 each
+// partition writes an f32 plane that t0mi_splitk_reduce sums.
+template <int WAVES, int KBW>
+__global__ __launch_bounds__(WAVES * 64) void w4a16_decode_kernel(W4Params p) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int c = lane & 15, g = lane >> 4;  // column quad, k sub-row (packed row within a k-block)
+  const int n0 = blockIdx.x * 64;
+  const int ncol = n0 + 4 * c;
+  const int kb_tot = (int)(p.K / 32);
+  const int kb_part0 = (int)(blockIdx.y * p.kb_per_split);
+  int kb_part1 = kb_part0 + (int)p.kb_per_split;
+  kb_part1 = kb_part1 < kb_tot ? kb_part1 : kb_tot;
+  const int kb0 = kb_part0 + wave * KBW;
+  const int kbpg = (int)(p.group / 32);
+  const bool col_ok = ncol < (int)p.N;
+  const int arow = c;  // activation row fed by this lane (A operand row = lane % 16)
+  const bool row_ok = arow < (int)p.M;
+
+  u32x4 wv[KBW], av[KBW];
+#pragma unroll
+  for (int b = 0; b < KBW; ++b) {
+    const int kb = kb0 + b;
+    u32x4 w = {0u, 0u, 0u, 0u}, a = {0u, 0u, 0u, 0u};
+    if (kb < kb_part1) {
+      if (col_ok) w = __builtin_nontemporal_load((const u32x4*)(p.w + (size_t)(kb * 4 + g) * p.N + ncol));
+      if (row_ok) a = *(const u32x4*)(p.a + (size_t)arow * p.K + kb * 32 + g * 8);
+    }
+    wv[b] = w;
+    av[b] = a;
+  }
+
+  const bf16x8_t ones = __builtin_bit_cast(bf16x8_t, (u32x4){0x3F803F80u, 0x3F803F80u, 0x3F803F80u, 0x3F803F80u});
+  f32x4 acc[4], P[4], S;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) acc[j] = (f32x4){0.f, 0.f, 0.f, 0.f};
+
+  // Output rows held by this lane: 4*g + r; columns ncol + j.
+#pragma unroll
+  for (int b = 0; b < KBW; ++b) {
+    const int kb = kb0 + b;
+    if (kb >= kb_part1) break;
+    if (b == 0 || (kb % kbpg) == 0) {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) P[j] = (f32x4){0.f, 0.f, 0.f, 0.f};
+      S = (f32x4){0.f, 0.f, 0.f, 0.f};
+    }
+    const bf16x8_t A = perm_act(av[b]);
+    S = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A, ones, S, 0, 0, 0);
+    P[0] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A, nib_pairs(wv[b].x), P[0], 0, 0, 0);
+    P[1] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A, nib_pairs(wv[b].y), P[1], 0, 0, 0);
+    P[2] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A, nib_pairs(wv[b].z), P[2], 0, 0, 0);
+    P[3] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A, nib_pairs(wv[b].w), P[3], 0, 0, 0);
+    if (((kb + 1) % kbpg) == 0 || kb + 1 == kb_part1 || b + 1 == KBW) {
+      // Group (or wave range) ends: y += s * (P - (128 + z) * S).
+      // Output column of P[j] for this lane is ncol' = n0 + 4*(lane & 15) + j,
+      // the same four columns this lane loaded.
+      const int grp = kb / kbpg;
+      float s[4], z[4];
+      if (col_ok) {
+        const u32x2 sv = *(const u32x2*)(p.scales + (size_t)grp * p.N + ncol);
+        s[0] = bf16f(sv.x & 0xFFFFu);
+        s[1] = bf16f(sv.x >> 16);
+        s[2] = bf16f(sv.y & 0xFFFFu);
+        s[3] = bf16f(sv.y >> 16);
+        if (p.zeros) {
+          const uint32_t zw = p.zeros[(size_t)grp * (p.N / 8) + ncol / 8] >> (4 * (ncol & 7));
+#pragma unroll
+          for (int j = 0; j < 4; ++j) z[j] = 128.0f + (float)((zw >> (4 * j)) & 0xFu);
+        } else {
+#pragma unroll
+          for (int j = 0; j < 4; ++j) z[j] = 128.0f + (float)p.zp_const;
+        }
+      } else {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) s[j] = 0.f, z[j] = 0.f;
+      }
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        acc[j].x += s[j] * (P[j].x - z[j] * S.x);
+        acc[j].y += s[j] * (P[j].y - z[j] * S.y);
+        acc[j].z += s[j] * (P[j].z - z[j] * S.z);
+        acc[j].w += s[j] * (P[j].w - z[j] * S.w);
+      }
+    }
+  }
+
+  // Cross-wave reduction in wave order.  red[wave][lane][16].
+  __shared__ float red[WAVES * 64 * 16];
+  float* mine = red + (wave * 64 + lane) * 16;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) *(f32x4*)(mine + 4 * j) = acc[j];
+  __syncthreads();
+  // Thread t < 64*16/4: handles lane L = t / 4 and word j = t % 4 (4 rows).
+  for (int t = threadIdx.x; t < 64 * 4; t += WAVES * 64) {
+    const int L = t >> 2, j = t & 3;
+    f32x4 s4 = *(const f32x4*)(red + (0 * 64 + L) * 16 + 4 * j);
+    for (int v = 1; v < WAVES; ++v) {
+      const f32x4 t4 = *(const f32x4*)(red + (v * 64 + L) * 16 + 4 * j);
+      s4.x += t4.x;
+      s4.y += t4.y;
+      s4.z += t4.z;
+      s4.w += t4.w;
+    }
+    const int col = n0 + 4 * (L & 15) + j;
+    const int row0 = 4 * (L >> 4);
+    if (col >= (int)p.N) continue;
+    const float vals[4] = {s4.x, s4.y, s4.z, s4.w};
+    if (gridDim.y > 1) {
+      float* yp = (float*)((char*)p.y + (size_t)blockIdx.y * p.y_split_stride);
+#pragma unroll
+      for (int r = 0; r < 4; ++r)
+        if (row0 + r < (int)p.M) yp[(size_t)(row0 + r) * p.N + col] = vals[r];
+    } else if (p.out_bf16) {
+      uint16_t* yp = (uint16_t*)p.y;
+#pragma unroll
+      for (int r = 0; r < 4; ++r)
+        if (row0 + r < (int)p.M) yp[(size_t)(row0 + r) * p.N + col] = f32_to_bf16_rne(vals[r]);
+    } else {
+      float* yp = (float*)p.y;
+#pragma unroll
+      for (int r = 0; r < 4; ++r)
+        if (row0 + r < (int)p.M) yp[(size_t)(row0 + r) * p.N + col] = vals[r];
+    }
+  }
+}
+
+// Standalone dequant (replaces build_dequant_int4_{f32,bf16}, quant_kernels.rs:53-171):
+// one thread per packed word -> 8 outputs down column n.  round_mode 0: f32,
+// 1: bf16 truncation (the reference's store_bf16), 2: bf16 RNE.
+__global__ __launch_bounds__(256) void dequant_int4_kernel(const uint32_t* __restrict__ w,
+                                                           const uint16_t* __restrict__ scales,
+                                                           const uint32_t* __restrict__ zeros, uint32_t zp_const,
+                                                           void* __restrict__ out, uint32_t K, uint32_t N,
+                                                           uint32_t group, uint32_t round_mode) {
+  const size_t words = (size_t)(K / 8) * N;
+  for (size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x; i < words; i += (size_t)gridDim.x * blockDim.x) {
+    const uint32_t kk = (uint32_t)(i / N), n = (uint32_t)(i % N);
+    const uint32_t word = w[i];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const uint32_t k = kk * 8 + e;
+      const uint32_t grp = k / group;
+      const int q = (int)((word >> (4 * e)) & 0xFu);
+      const int z = zeros ? (int)((zeros[(size_t)grp * (N / 8) + n / 8] >> (4 * (n & 7))) & 0xFu) : (int)zp_const;
+      const float v = (float)(q - z) * bf16f(scales[(size_t)grp * N + n]);
+      const size_t o = (size_t)k * N + n;
+      if (round_mode == 0)
+        ((float*)out)[o] = v;
+      else if (round_mode == 1)
+        ((uint16_t*)out)[o] = (uint16_t)(__builtin_bit_cast(uint32_t, v) >> 16);
+      else
+        ((uint16_t*)out)[o] = f32_to_bf16_rne(v);
+    }
+  }
+}
+
+}  // namespace t0mi
+
+static int hip_fail(hipError_t e, const char* what) {
+  return set_error(T0MI_ERR_HIP, "%s: %s", what, hipGetErrorString(e));
+}
+
+extern "C" int t0mi_w4a16_gemm(t0mi_ctx* ctx, uint64_t a, uint64_t qweight, uint64_t scales, uint64_t qzeros,
+                               uint32_t zp_const, uint64_t y, uint32_t m, uint32_t k, uint32_t n, uint32_t group,
+                               uint32_t out_dtype) {
+  int rc = check_ctx(ctx);
+  if (rc) return rc;
+  if (!a || !qweight || !scales || !y) return set_error(T0MI_ERR_INVALID, "null pointer");
+  if (group == 0 || group % 32) return set_error(T0MI_ERR_INVALID, "group=%u must be a positive multiple of 32", group);
+  if (k % group) return set_error(T0MI_ERR_INVALID, "K=%u must be a multiple of group=%u", k, group);
+  if (n % 8) return set_error(T0MI_ERR_INVALID, "N=%u must be a multiple of 8", n);
+  if (zp_const > 15) return set_error(T0MI_ERR_INVALID, "zp_const=%u outside 0..15", zp_const);
+  if (out_dtype > T0MI_OUT_BF16) return set_error(T0MI_ERR_INVALID, "bad out_dtype");
+  if ((a | qweight) & 15) return set_error(T0MI_ERR_INVALID, "A and qweight must be 16-byte aligned");
+  if ((scales & 7) || (y & 7)) return set_error(T0MI_ERR_INVALID, "scales and Y must be 8-byte aligned");
+  if (m == 0 || n == 0) return T0MI_OK;
+  if (ctx->null_backend) return T0MI_OK;
+  W4Params p;
+  memset(&p, 0, sizeof p);
+  p.a = (const uint16_t*)a;
+  p.w = (const uint32_t*)qweight;
+  p.scales = (const uint16_t*)scales;
+  p.zeros = (const uint32_t*)qzeros;
+  p.K = k;
+  p.N = n;
+  p.group = group;
+  p.zp_const = zp_const;
+  p.out_bf16 = out_dtype == T0MI_OUT_BF16;
+  constexpr int WAVES = 8, KBW = 16;
+  const uint32_t kb_tot = k / 32;
+  const uint32_t ky = (kb_tot + WAVES * KBW - 1) / (WAVES * KBW);
+  p.kb_per_split = WAVES * KBW;
+  const uint32_t strips = (n + 63) / 64;
+  // Row slabs of 16: the decode kernel is launched once per slab.
+  for (uint32_t r0 = 0; r0 < m; r0 += 16) {
+    const uint32_t mr = std::min(16u, m - r0);
+    p.a = (const uint16_t*)a + (size_t)r0 * k;
+    p.M = mr;
+    const size_t ob = out_dtype == T0MI_OUT_BF16 ? 2 : 4;
+    if (ky > 1) {
+      const size_t plane = (size_t)mr * n * 4;
+      rc = ensure_workspace(ctx, plane * ky);
+      if (rc) return rc;
+      p.y = ctx->ws;
+      p.y_split_stride = plane;
+    } else {
+      p.y = (char*)y + (size_t)r0 * n * ob;
+    }
+    hipLaunchKernelGGL((w4a16_decode_kernel<WAVES, KBW>), dim3(strips, ky), dim3(WAVES * 64), 0, ctx->stream, p);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return hip_fail(e, "w4a16 launch");
+    if (ky > 1) {
+      rc = launch_splitk_reduce(ctx, (const float*)ctx->ws, (char*)y + (size_t)r0 * n * ob, nullptr, mr, n, n, ky,
+                                p.out_bf16, 0u);
+      if (rc) return rc;
+    }
+  }
+  return T0MI_OK;
+}
+
+extern "C" int t0mi_dequant_int4(t0mi_ctx* ctx, uint64_t qweight, uint64_t scales, uint64_t qzeros, uint32_t zp_const,
+                                 uint64_t out, uint32_t k, uint32_t n, uint32_t group, uint32_t round_mode) {
+  int rc = check_ctx(ctx);
+  if (rc) return rc;
+  if (!qweight || !scales || !out) return set_error(T0MI_ERR_INVALID, "null pointer");
+  if (group == 0 || k % group || k % 8) return set_error(T0MI_ERR_INVALID, "K=%u must be a multiple of group=%u and 8", k, group);
+  if (n % 8) return set_error(T0MI_ERR_INVALID, "N=%u must be a multiple of 8", n);
+  if (round_mode > 2) return set_error(T0MI_ERR_INVALID, "round_mode=%u (0 f32, 1 bf16 trunc, 2 bf16 rne)", round_mode);
+  if (zp_const > 15) return set_error(T0MI_ERR_INVALID, "zp_const=%u outside 0..15", zp_const);
+  if (ctx->null_backend || k == 0 || n == 0) return T0MI_OK;
+  const size_t words = (size_t)(k / 8) * n;
+  const uint32_t blocks = (uint32_t)std::min<size_t>((words + 255) / 256, (size_t)ctx->cu_count * 16);
+  hipLaunchKernelGGL(dequant_int4_kernel, dim3(blocks), dim3(256), 0, ctx->stream, (const uint32_t*)qweight,
+                     (const uint16_t*)scales, (const uint32_t*)qzeros, zp_const, (void*)out, k, n, group, round_mode);
+  hipError_t e = hipGetLastError();
+  return e == hipSuccess ? T0MI_OK : hip_fail(e, "dequant launch");
+}

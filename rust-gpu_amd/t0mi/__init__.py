@@ -1,0 +1,404 @@
+"""t0mi — Python binding of libt0mi, the gfx950 GEMM hot path of T0-GPU.
+
+The product is the C ABI in ``include/t0mi.h`` (implemented in
+``rust-gpu_amd/csrc``); this module is a thin ``ctypes`` layer over it for
+tests, the benchmark and Python callers.  Names follow the reference's Rust
+API (``GemmConfig``, ``auto_select``, ``GemmTuner.tune``, ``GpuRuntime``
+dispatch); each wrapper names the reference item it mirrors.
+
+There is no fallback: if ``libt0mi.so`` is missing, importing this module
+raises, and every compute call goes through the HIP kernels in the library.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import subprocess
+from typing import Optional, Sequence
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+_PKG_ROOT = os.path.dirname(_HERE)
+LIB_PATH = os.path.join(_HERE, "libt0mi.so")
+
+OK = 0
+ERR_INVALID, ERR_NO_KERNEL, ERR_HIP, ERR_POISONED, ERR_KERNARG, ERR_TIMEOUT, ERR_NOT_FOUND, ERR_NO_DEVICE = \
+    -1, -2, -3, -4, -5, -6, -7, -8
+NT, NN = 0, 1
+EPI_STORE_F32, EPI_BIAS_ADD, EPI_BIAS_ADD_RELU = 0, 1, 2
+OUT_F32, OUT_BF16 = 0, 1
+
+
+def build(jobs: int = 8) -> str:
+    """Compile libt0mi.so for gfx950 with the package Makefile (always rebuilds stale objects)."""
+    subprocess.run(["make", "-s", f"-j{jobs}", "-C", _PKG_ROOT], check=True)
+    return LIB_PATH
+
+
+class T0miError(RuntimeError):
+    def __init__(self, code: int, msg: str):
+        super().__init__(f"t0mi error {code}: {msg}")
+        self.code = code
+
+
+class GemmConfig(ctypes.Structure):
+    """Mirror of ``GemmConfig`` (src/t0/gemm_gen.rs:55-84) plus gfx950 fields."""
+    _fields_ = [(n, ctypes.c_uint32) for n in (
+        "tile_m", "tile_n", "tile_k", "wg_size", "use_lds", "double_buffer", "split_k", "lds_pad",
+        "n_col_passes", "swap_grid", "wgp_mode", "transpose", "epilogue", "out_dtype", "wave_m", "wave_n")]
+
+    def copy(self, **kw) -> "GemmConfig":
+        c = GemmConfig()
+        ctypes.memmove(ctypes.byref(c), ctypes.byref(self), ctypes.sizeof(GemmConfig))
+        for k, v in kw.items():
+            setattr(c, k, v)
+        return c
+
+    def name(self) -> str:
+        return config_name(self)
+
+    def is_feasible(self) -> bool:
+        return bool(lib().t0mi_config_is_feasible(ctypes.byref(self)))
+
+    def as_dict(self) -> dict:
+        return {n: getattr(self, n) for n, _ in self._fields_}
+
+    def __repr__(self):
+        return f"GemmConfig({self.name()})"
+
+
+_lib = None
+
+# Every symbol declared in include/t0mi.h, with (restype, argtypes).
+_P = ctypes.c_void_p
+_U32 = ctypes.c_uint32
+_U64 = ctypes.c_uint64
+_SZ = ctypes.c_size_t
+_I = ctypes.c_int
+_CFG = ctypes.POINTER(GemmConfig)
+_CHARP = ctypes.c_char_p
+SIGNATURES = {
+    "t0mi_last_error": (_CHARP, []),
+    "t0mi_abi_version": (_I, []),
+    "t0mi_build_target": (_CHARP, []),
+    "t0mi_config_preset": (_I, [_CHARP, _CFG]),
+    "t0mi_config_preset_names": (_I, [_CHARP, _SZ]),
+    "t0mi_config_n_waves": (_U32, [_CFG]),
+    "t0mi_config_lds_total": (_U32, [_CFG]),
+    "t0mi_config_estimated_regs": (_U32, [_CFG]),
+    "t0mi_config_is_feasible": (_I, [_CFG]),
+    "t0mi_config_name": (_I, [_CFG, _CHARP, _SZ]),
+    "t0mi_compute_grid": (_I, [_CFG, _U32, _U32, ctypes.POINTER(_U32)]),
+    "t0mi_compute_grid_split_k": (_I, [_CFG, _U32, _U32, _U32, ctypes.POINTER(_U32)]),
+    "t0mi_compute_grid_auto": (_I, [_CFG, _U32, _U32, ctypes.POINTER(_U32)]),
+    "t0mi_build_kernargs": (_I, [_U64, _U64, _U64, _U32, _U32, _U32, _CFG, _P]),
+    "t0mi_build_kernargs_with_bias": (_I, [_U64, _U64, _U64, _U32, _U32, _U32, _CFG, _U64, _P]),
+    "t0mi_auto_select": (_I, [_U32, _U32, _U32, _CFG]),
+    "t0mi_auto_select_legacy": (_I, [_U32, _U32, _U32, _CFG]),
+    "t0mi_cached_auto_select": (_I, [_U32, _U32, _U32, _CFG]),
+    "t0mi_clear_spec_cache": (None, []),
+    "t0mi_spec_cache_len": (_SZ, []),
+    "t0mi_ctx_create": (_I, [_I, ctypes.POINTER(_P)]),
+    "t0mi_ctx_create_on_stream": (_I, [_I, _P, ctypes.POINTER(_P)]),
+    "t0mi_ctx_create_null": (_I, [ctypes.POINTER(_P)]),
+    "t0mi_ctx_destroy": (None, [_P]),
+    "t0mi_ctx_stream": (_P, [_P]),
+    "t0mi_is_poisoned": (_I, [_P]),
+    "t0mi_mark_poisoned": (None, [_P]),
+    "t0mi_set_timeout_ms": (None, [_P, _U32]),
+    "t0mi_null_inject_timeout": (_I, [_P]),
+    "t0mi_null_last_dispatch": (_I, [_P, ctypes.POINTER(_U32), _P, _SZ, ctypes.POINTER(_SZ)]),
+    "t0mi_alloc": (_I, [_P, _SZ, ctypes.POINTER(_U64)]),
+    "t0mi_alloc_zero": (_I, [_P, _SZ, ctypes.POINTER(_U64)]),
+    "t0mi_free": (_I, [_P, _U64]),
+    "t0mi_h2d": (_I, [_P, _U64, _P, _SZ]),
+    "t0mi_d2h": (_I, [_P, _P, _U64, _SZ]),
+    "t0mi_memset": (_I, [_P, _U64, _I, _SZ]),
+    "t0mi_kernel_get": (_I, [_P, _CFG, ctypes.POINTER(_P)]),
+    "t0mi_kernel_attrs": (_I, [_P, ctypes.POINTER(_U32), ctypes.POINTER(_U32), ctypes.POINTER(_U32)]),
+    "t0mi_kernel_name": (_I, [_P, _CHARP, _SZ]),
+    "t0mi_dispatch": (_I, [_P, _P, ctypes.POINTER(_U32), _P, _SZ]),
+    "t0mi_dispatch_async": (_I, [_P, _P, ctypes.POINTER(_U32), _P, _SZ]),
+    "t0mi_wait_idle": (_I, [_P]),
+    "t0mi_gemm": (_I, [_P, _CFG, _U64, _U64, _U64, _U64, _U32, _U32, _U32]),
+    "t0mi_tuner_create": (_I, [_CHARP, ctypes.POINTER(_P)]),
+    "t0mi_tuner_destroy": (None, [_P]),
+    "t0mi_tuner_set_params": (None, [_P, _U32, _U32]),
+    "t0mi_tuner_tune": (_I, [_P, _P, _U32, _U32, _U32, _U32, _U32, _CFG, ctypes.POINTER(ctypes.c_double),
+                             ctypes.POINTER(_I)]),
+    "t0mi_tuner_invalidate": (None, [_P, _U32, _U32, _U32, _U32, _U32]),
+    "t0mi_tuner_clear": (None, [_P]),
+    "t0mi_tuner_cache_path": (_I, [_P, _U32, _U32, _U32, _U32, _U32, _CHARP, _SZ]),
+    "t0mi_tuner_report": (_I, [_P, _CHARP, _SZ]),
+    "t0mi_auto_gemm": (_I, [_P, _U64, _U64, _U64, _U32, _U32, _U32, ctypes.POINTER(ctypes.c_double)]),
+    "t0mi_w4a16_gemm": (_I, [_P, _U64, _U64, _U64, _U64, _U32, _U64, _U32, _U32, _U32, _U32, _U32]),
+    "t0mi_dequant_int4": (_I, [_P, _U64, _U64, _U64, _U32, _U64, _U32, _U32, _U32, _U32]),
+}
+
+
+def lib():
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise ImportError(f"libt0mi.so not built at {LIB_PATH}; run __graft_entry__.build() "
+                              f"(make -C {_PKG_ROOT})")
+        L = ctypes.CDLL(LIB_PATH)
+        for name, (res, args) in SIGNATURES.items():
+            f = getattr(L, name)
+            f.restype = res
+            f.argtypes = args
+        _lib = L
+    return _lib
+
+
+def last_error() -> str:
+    return lib().t0mi_last_error().decode()
+
+
+def check(rc: int) -> int:
+    if rc != OK:
+        raise T0miError(rc, last_error())
+    return rc
+
+
+# ------------------------------------------------------------- config ----
+
+def preset(name: str) -> GemmConfig:
+    """``GemmConfig::tile_*()`` presets (src/t0/gemm_gen.rs:87-145) and gfx950 presets."""
+    c = GemmConfig()
+    check(lib().t0mi_config_preset(name.encode(), ctypes.byref(c)))
+    return c
+
+
+def preset_names() -> list:
+    buf = ctypes.create_string_buffer(4096)
+    lib().t0mi_config_preset_names(buf, 4096)
+    return buf.value.decode().split(",")
+
+
+def config_name(cfg: GemmConfig) -> str:
+    buf = ctypes.create_string_buffer(256)
+    check_len = lib().t0mi_config_name(ctypes.byref(cfg), buf, 256)
+    if check_len < 0:
+        raise T0miError(check_len, last_error())
+    return buf.value.decode()
+
+
+def lds_total(cfg: GemmConfig) -> int:
+    return lib().t0mi_config_lds_total(ctypes.byref(cfg))
+
+
+def compute_grid(cfg: GemmConfig, m: int, n: int):
+    g = (ctypes.c_uint32 * 2)()
+    check(lib().t0mi_compute_grid(ctypes.byref(cfg), m, n, g))
+    return (g[0], g[1])
+
+
+def compute_grid_split_k(cfg: GemmConfig, m: int, n: int, split_k: int):
+    g = (ctypes.c_uint32 * 2)()
+    check(lib().t0mi_compute_grid_split_k(ctypes.byref(cfg), m, n, split_k, g))
+    return (g[0], g[1])
+
+
+def compute_grid_auto(cfg: GemmConfig, m: int, n: int):
+    g = (ctypes.c_uint32 * 2)()
+    check(lib().t0mi_compute_grid_auto(ctypes.byref(cfg), m, n, g))
+    return (g[0], g[1])
+
+
+def build_kernargs(x: int, wt: int, y: int, k: int, n: int, m: int, cfg: GemmConfig) -> bytes:
+    """``gemm_gen::build_kernargs(x, wt, y, k, n, m, cfg)`` — 40 bytes (gemm_gen.rs:439-458)."""
+    buf = (ctypes.c_uint8 * 40)()
+    check(lib().t0mi_build_kernargs(x, wt, y, k, n, m, ctypes.byref(cfg), buf))
+    return bytes(buf)
+
+
+def build_kernargs_with_bias(x: int, wt: int, y: int, k: int, n: int, m: int, cfg: GemmConfig, bias: int) -> bytes:
+    buf = (ctypes.c_uint8 * 48)()
+    check(lib().t0mi_build_kernargs_with_bias(x, wt, y, k, n, m, ctypes.byref(cfg), bias, buf))
+    return bytes(buf)
+
+
+def auto_select(m: int, k: int, n: int) -> GemmConfig:
+    """``gemm_gen::auto_select(m, k, n)`` — note the (m, k, n) order."""
+    c = GemmConfig()
+    check(lib().t0mi_auto_select(m, k, n, ctypes.byref(c)))
+    return c
+
+
+def auto_select_legacy(m: int, k: int, n: int) -> GemmConfig:
+    c = GemmConfig()
+    check(lib().t0mi_auto_select_legacy(m, k, n, ctypes.byref(c)))
+    return c
+
+
+def cached_auto_select(m: int, k: int, n: int) -> GemmConfig:
+    c = GemmConfig()
+    check(lib().t0mi_cached_auto_select(m, k, n, ctypes.byref(c)))
+    return c
+
+
+# ------------------------------------------------------------ runtime ----
+
+class Kernel:
+    """``GpuKernel`` — a prebuilt gfx950 kernel looked up by config name."""
+
+    def __init__(self, handle, rt):
+        self.handle = handle
+        self._rt = rt  # keeps the owning runtime alive
+
+    def attrs(self):
+        lds, wg, ka = ctypes.c_uint32(), ctypes.c_uint32(), ctypes.c_uint32()
+        check(lib().t0mi_kernel_attrs(self.handle, ctypes.byref(lds), ctypes.byref(wg), ctypes.byref(ka)))
+        return {"lds_size": lds.value, "wg_size": wg.value, "kernarg_size": ka.value}
+
+    @property
+    def name(self) -> str:
+        buf = ctypes.create_string_buffer(256)
+        lib().t0mi_kernel_name(self.handle, buf, 256)
+        return buf.value.decode()
+
+
+class Runtime:
+    """``GpuRuntime`` (src/ignis/gpu_context.rs:99-545) over HIP."""
+
+    def __init__(self, device: int = -1, stream: Optional[int] = None, null: bool = False):
+        h = ctypes.c_void_p()
+        if null:
+            check(lib().t0mi_ctx_create_null(ctypes.byref(h)))
+        elif stream is not None:
+            check(lib().t0mi_ctx_create_on_stream(device, ctypes.c_void_p(stream), ctypes.byref(h)))
+        else:
+            check(lib().t0mi_ctx_create(device, ctypes.byref(h)))
+        self.handle = h
+
+    @classmethod
+    def on_torch_stream(cls, device: int = 0):
+        import torch
+        return cls(device=device, stream=torch.cuda.current_stream(device).cuda_stream)
+
+    def close(self):
+        if self.handle:
+            lib().t0mi_ctx_destroy(self.handle)
+            self.handle = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    @property
+    def stream(self) -> int:
+        return lib().t0mi_ctx_stream(self.handle) or 0
+
+    def is_poisoned(self) -> bool:
+        return bool(lib().t0mi_is_poisoned(self.handle))
+
+    def mark_poisoned(self):
+        lib().t0mi_mark_poisoned(self.handle)
+
+    def set_timeout_ms(self, ms: int):
+        lib().t0mi_set_timeout_ms(self.handle, ms)
+
+    def inject_timeout(self):
+        check(lib().t0mi_null_inject_timeout(self.handle))
+
+    def last_dispatch(self):
+        g = (ctypes.c_uint32 * 3)()
+        buf = (ctypes.c_uint8 * 256)()
+        n = ctypes.c_size_t()
+        check(lib().t0mi_null_last_dispatch(self.handle, g, buf, 256, ctypes.byref(n)))
+        return (g[0], g[1], g[2]), bytes(buf[: n.value])
+
+    # memory
+    def alloc(self, nbytes: int, zero: bool = False) -> int:
+        p = ctypes.c_uint64()
+        f = lib().t0mi_alloc_zero if zero else lib().t0mi_alloc
+        check(f(self.handle, nbytes, ctypes.byref(p)))
+        return p.value
+
+    def free(self, dptr: int):
+        check(lib().t0mi_free(self.handle, dptr))
+
+    def h2d(self, dptr: int, host_bytes) -> None:
+        import numpy as np
+        arr = np.ascontiguousarray(host_bytes)
+        check(lib().t0mi_h2d(self.handle, dptr, arr.ctypes.data_as(ctypes.c_void_p), arr.nbytes))
+
+    def d2h(self, dptr: int, out) -> None:
+        check(lib().t0mi_d2h(self.handle, out.ctypes.data_as(ctypes.c_void_p), dptr, out.nbytes))
+
+    # kernels
+    def kernel(self, cfg: GemmConfig) -> Kernel:
+        """``ensure_kernel_t0(cfg.name(), || generate(&cfg), ..)`` -> prebuilt kernel."""
+        h = ctypes.c_void_p()
+        check(lib().t0mi_kernel_get(self.handle, ctypes.byref(cfg), ctypes.byref(h)))
+        return Kernel(h, self)
+
+    def dispatch(self, k: Kernel, grid: Sequence[int], ka: bytes, sync: bool = True) -> int:
+        g = (ctypes.c_uint32 * 3)(*(list(grid) + [1] * (3 - len(grid))))
+        buf = (ctypes.c_uint8 * max(1, len(ka))).from_buffer_copy(ka or b"\0")
+        f = lib().t0mi_dispatch if sync else lib().t0mi_dispatch_async
+        return f(self.handle, k.handle, g, buf, len(ka))
+
+    def wait_idle(self) -> int:
+        return lib().t0mi_wait_idle(self.handle)
+
+    def gemm(self, cfg: GemmConfig, x: int, b: int, y: int, m: int, n: int, k: int, bias: int = 0) -> None:
+        check(lib().t0mi_gemm(self.handle, ctypes.byref(cfg), x, b, y, bias, m, n, k))
+
+    def w4a16_gemm(self, a: int, qweight: int, scales: int, qzeros: int, zp_const: int, y: int,
+                   m: int, k: int, n: int, group: int, out_dtype: int = OUT_BF16) -> None:
+        check(lib().t0mi_w4a16_gemm(self.handle, a, qweight, scales, qzeros, zp_const, y, m, k, n, group, out_dtype))
+
+    def dequant_int4(self, qweight: int, scales: int, qzeros: int, zp_const: int, out: int,
+                     k: int, n: int, group: int, round_mode: int) -> None:
+        check(lib().t0mi_dequant_int4(self.handle, qweight, scales, qzeros, zp_const, out, k, n, group, round_mode))
+
+    def auto_gemm(self, a: int, b: int, c: int, m: int, n: int, k: int) -> float:
+        tf = ctypes.c_double()
+        check(lib().t0mi_auto_gemm(self.handle, a, b, c, m, n, k, ctypes.byref(tf)))
+        return tf.value
+
+
+class GemmTuner:
+    """``GemmTuner`` (src/t0/auto_gemm.rs:46-527)."""
+
+    def __init__(self, cache_dir: Optional[str] = None, max_candidates: int = 8, n_iters: int = 5):
+        h = ctypes.c_void_p()
+        check(lib().t0mi_tuner_create(cache_dir.encode() if cache_dir else None, ctypes.byref(h)))
+        self.handle = h
+        lib().t0mi_tuner_set_params(h, max_candidates, n_iters)
+
+    def __del__(self):
+        try:
+            if self.handle:
+                lib().t0mi_tuner_destroy(self.handle)
+                self.handle = None
+        except Exception:
+            pass
+
+    def tune(self, rt: Runtime, m: int, n: int, k: int, transpose: int = NT, out_dtype: int = OUT_F32):
+        """``GemmTuner::tune(rt, m, n, k)`` -> (config, tflops, from_cache)."""
+        c = GemmConfig()
+        tf = ctypes.c_double()
+        fc = ctypes.c_int()
+        check(lib().t0mi_tuner_tune(self.handle, rt.handle, m, n, k, transpose, out_dtype, ctypes.byref(c),
+                                    ctypes.byref(tf), ctypes.byref(fc)))
+        return c, tf.value, bool(fc.value)
+
+    def invalidate(self, m, n, k, transpose=NT, out_dtype=OUT_F32):
+        lib().t0mi_tuner_invalidate(self.handle, m, n, k, transpose, out_dtype)
+
+    def clear(self):
+        lib().t0mi_tuner_clear(self.handle)
+
+    def cache_path(self, m, n, k, transpose=NT, out_dtype=OUT_F32) -> str:
+        buf = ctypes.create_string_buffer(1024)
+        lib().t0mi_tuner_cache_path(self.handle, m, n, k, transpose, out_dtype, buf, 1024)
+        return buf.value.decode()
+
+    def report(self) -> str:
+        buf = ctypes.create_string_buffer(65536)
+        lib().t0mi_tuner_report(self.handle, buf, 65536)
+        return buf.value.decode()

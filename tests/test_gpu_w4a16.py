@@ -1,0 +1,129 @@
+"""GPU parity tests of the W4A16 GEMM and the standalone INT4 dequant against the oracle.
+
+Bars: dequant bit-exact (f32, bf16-truncate, bf16-RNE); GEMM within
+max|err| <= 1e-2 * sqrt(K) * max|a| * max|w| with relative Frobenius error bounded.
+"""
+import numpy as np
+import pytest
+
+import oracle
+import t0mi
+from gpu_helpers import empty_dev, from_dev, runtime, to_dev
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def rt():
+    r = runtime()
+    yield r
+    r.close()
+
+
+def make_case(m, k, n, group, per_group_zeros, seed=0x40):
+    a = oracle.normal_bf16((m, k), seed + 1, 0.0, 1.0)
+    q = oracle.nibbles((k, n), seed + 2)
+    w = oracle.pack_qweight(q)
+    s = oracle.uniform_bf16((k // group, n), seed + 3, 0.005, 0.02)
+    z = oracle.pack_qzeros(oracle.nibbles((k // group, n), seed + 4)) if per_group_zeros else None
+    return a, q, w, s, z
+
+
+def run_w4a16(rt, a, w, s, z, m, k, n, group, zp_const=8, out_bf16=True):
+    da, pa = to_dev(a)
+    dw, pw = to_dev(w)
+    ds, ps = to_dev(s)
+    pz = 0
+    if z is not None:
+        dz, pz = to_dev(z)
+    ob = 2 if out_bf16 else 4
+    dy, py = empty_dev(m * n * ob, fill=0xCD)
+    rt.w4a16_gemm(pa, pw, ps, pz, zp_const, py, m, k, n, group, t0mi.OUT_BF16 if out_bf16 else t0mi.OUT_F32)
+    y = from_dev(dy, np.uint16 if out_bf16 else np.float32, (m, n))
+    return oracle.bf16_to_f32(y) if out_bf16 else y
+
+
+def check(y, ref, a, wf, k, rel_max):
+    tol = oracle.gemm_tolerance(k, oracle.bf16_to_f32(a), wf)
+    err, rel = oracle.compare(y, ref)
+    assert err <= tol, (err, tol)
+    assert rel <= rel_max, rel
+    return err, rel
+
+
+@pytest.mark.parametrize("m,k,n,group,pgz", [
+    (16, 4096, 11008, 128, False),   # BASELINE config 4 (decode), full size
+    (1, 512, 64, 128, False),
+    (5, 256, 136, 32, True),
+    (16, 1024, 520, 64, True),
+    (16, 8192, 256, 128, False),     # K beyond one workgroup's range -> split + reduce
+    (37, 384, 200, 128, True),       # M > 16 -> several row slabs
+    (3, 4096, 64, 4096, False),      # group larger than a wave's K range
+])
+def test_w4a16_vs_oracle(rt, m, k, n, group, pgz):
+    a, q, w, s, z = make_case(m, k, n, group, pgz)
+    ref = oracle.w4a16_gemm(a, w, s, z, group, 8)
+    wf = oracle.dequant_qweight_f32(w, s, z, group, 8)
+    y32 = run_w4a16(rt, a, w, s, z, m, k, n, group, out_bf16=False)
+    check(y32, ref, a, wf, k, 1e-5)
+    yb = run_w4a16(rt, a, w, s, z, m, k, n, group, out_bf16=True)
+    check(yb, ref, a, wf, k, 5e-3)
+
+
+def test_w4a16_deterministic(rt):
+    m, k, n, group = 16, 4096, 1024, 128
+    a, q, w, s, z = make_case(m, k, n, group, False, seed=0x90)
+    y1 = run_w4a16(rt, a, w, s, z, m, k, n, group, out_bf16=False)
+    y2 = run_w4a16(rt, a, w, s, z, m, k, n, group, out_bf16=False)
+    assert np.array_equal(y1.view(np.uint32), y2.view(np.uint32))
+
+
+def test_w4a16_integer_exact(rt):
+    """Small integer activations and power-of-two scales make every sum exact:
+    the fused kernel must then match the oracle bit for bit."""
+    m, k, n, group = 16, 512, 128, 128
+    rng = np.random.default_rng(5)
+    a = oracle.bf16_trunc(rng.integers(-3, 4, size=(m, k)).astype(np.float32))
+    q = oracle.nibbles((k, n), 77)
+    w = oracle.pack_qweight(q)
+    s = oracle.bf16_trunc(np.full((k // group, n), 0.25, np.float32))
+    zq = oracle.nibbles((k // group, n), 78)
+    z = oracle.pack_qzeros(zq)
+    ref = oracle.w4a16_gemm(a, w, s, z, group, 0)
+    y = run_w4a16(rt, a, w, s, z, m, k, n, group, out_bf16=False)
+    assert np.array_equal(y, ref)
+
+
+@pytest.mark.parametrize("round_mode", [0, 1, 2])
+@pytest.mark.parametrize("pgz", [False, True])
+def test_dequant_bit_exact(rt, round_mode, pgz):
+    k, n, group = 512, 264, 128
+    q = oracle.nibbles((k, n), 31)
+    w = oracle.pack_qweight(q)
+    s = oracle.uniform_bf16((k // group, n), 32, -0.05, 0.05)
+    z = oracle.pack_qzeros(oracle.nibbles((k // group, n), 33)) if pgz else None
+    ref = oracle.dequant_qweight_f32(w, s, z, group, 8)
+    dw, pw = to_dev(w)
+    ds, ps = to_dev(s)
+    pz = 0
+    if z is not None:
+        dz, pz = to_dev(z)
+    ob = 4 if round_mode == 0 else 2
+    dy, py = empty_dev(k * n * ob, fill=0)
+    rt.dequant_int4(pw, ps, pz, 8, py, k, n, group, round_mode)
+    if round_mode == 0:
+        got = from_dev(dy, np.float32, (k, n))
+        assert np.array_equal(got.view(np.uint32), ref.view(np.uint32))
+    else:
+        got = from_dev(dy, np.uint16, (k, n))
+        want = oracle.bf16_trunc(ref) if round_mode == 1 else oracle.bf16_rne(ref)
+        assert np.array_equal(got, want)
+
+
+def test_w4a16_rejects_bad_shapes(rt):
+    with pytest.raises(t0mi.T0miError):
+        rt.w4a16_gemm(16, 16, 16, 0, 8, 16, 16, 4096, 100, 128)   # N % 8 != 0
+    with pytest.raises(t0mi.T0miError):
+        rt.w4a16_gemm(16, 16, 16, 0, 8, 16, 16, 4000, 128, 128)  # K % group != 0
+    with pytest.raises(t0mi.T0miError):
+        rt.w4a16_gemm(16, 16, 16, 0, 8, 16, 16, 4096, 128, 48)   # group % 32 != 0
