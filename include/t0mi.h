@@ -60,9 +60,9 @@ typedef enum {                                                        /* gemm_ge
 typedef enum { T0MI_OUT_F32 = 0, T0MI_OUT_BF16 = 1 } t0mi_out_dtype; /* new: bf16 store, RNE */
 
 /* Field-for-field mirror of GemmConfig (gemm_gen.rs:55-84).  Booleans are
- * uint32_t 0/1; split_k 0 or 1 means None.  The last three fields are gfx950
+ * uint32_t 0/1; split_k 0 or 1 means None.  The last four fields are gfx950
  * extensions with no reference counterpart; zero keeps reference behaviour
- * (f32 output, wave layout derived from wg_size).
+ * (f32 output, wave layout derived from wg_size, two LDS stages).
  * wg_size is the real workgroup size in threads (64-wide waves on gfx950);
  * the reference's wave32 presets with wg_size 32 are infeasible here. */
 typedef struct t0mi_gemm_config {
@@ -75,6 +75,7 @@ typedef struct t0mi_gemm_config {
   uint32_t epilogue;  /* t0mi_epilogue */
   uint32_t out_dtype; /* t0mi_out_dtype (gfx950 extension) */
   uint32_t wave_m, wave_n; /* waves along M and N; 0,0 = derive (gfx950 extension) */
+  uint32_t stages;    /* LDS pipeline stages 2..5; 0 = 2 (double_buffer) (gfx950 extension) */
 } t0mi_gemm_config;
 
 /* Presets by reference name, e.g. "tile_128x64_k16" (gemm_gen.rs:87-145), plus
@@ -83,6 +84,11 @@ typedef struct t0mi_gemm_config {
 int t0mi_config_preset(const char* name, t0mi_gemm_config* out);
 /* Comma-separated preset names; writes at most len bytes (NUL-terminated). */
 int t0mi_config_preset_names(char* buf, size_t len);
+/* The prebuilt gfx950 kernels (the set a config must hit for t0mi_kernel_get):
+ * comma-separated "tile_m x tile_n x tile_k _w wave_m x wave_n _s stages [_nn]"
+ * entries, e.g. "256x256x64_w2x4_s2_nn".  No reference counterpart (the reference
+ * generates any config at run time); used by tuners and sweeps. */
+int t0mi_gemm_variants(char* buf, size_t len);
 /* Derived quantities (gemm_gen.rs:147-201). */
 uint32_t t0mi_config_n_waves(const t0mi_gemm_config* cfg);
 uint32_t t0mi_config_lds_total(const t0mi_gemm_config* cfg);

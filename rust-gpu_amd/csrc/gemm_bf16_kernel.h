@@ -3,21 +3,30 @@
 // Replaces the RDNA WMMA kernels that the reference generates at run time:
 //   src/t0/gemm_gen.rs:668-1438   (generate_lds_db)
 //   src/t0/tile_ir.rs:887-4250    (lower_gemm)
-// Same math — Y[M,N] = X[M,K] . B, bf16 inputs, fp32 accumulation — but laid
-// out for CDNA4: 64-wide waves, v_mfma_f32_32x32x16_bf16, a double-buffered
-// LDS tile with an XOR swizzle, 128-bit global loads and a K loop that issues
-// the next tile's global loads before the current tile's MFMAs.
+// Same math — Y[M,N] = X[M,K] . B, bf16 inputs, fp32 accumulation — laid out
+// for CDNA4:
+//   * global -> LDS with global_load_lds_dwordx4 (no VGPR staging, no ds_write):
+//     each wave instruction fills one contiguous 1 KB LDS block, so the LDS
+//     swizzle is applied on the global side (each lane fetches the chunk that
+//     belongs at its LDS slot);
+//   * double-buffered LDS tiles, one barrier per K tile, the next tile's loads
+//     issued before the current tile's MFMAs;
+//   * v_mfma_f32_32x32x16_bf16 with the A and B fragments of the next k-step
+//     read from LDS while the current k-step's MFMAs run.
 //
 // Layouts:
-//   A  = X[M,K] row-major (lda = K).
-//   NT: B = WT[N,K] row-major (ldb = K)  — the reference's only implemented layout.
-//   NN: B = B[K,N] row-major (ldb = N)   — BASELINE.json's layout.  8x8 blocks are
-//       transposed in registers (v_perm_b32) on their way into LDS, so both
-//       layouts reach the MFMA loop as K-contiguous LDS rows.
+//   A  = X[M,K] row-major (lda = K); LDS tile [BM][BK], 16-byte chunks XOR-swizzled
+//        per row, fragments read with ds_read_b128.
+//   NT: B = WT[N,K] row-major (ldb = K) — the reference's only implemented layout;
+//        LDS tile [BN][BK] like A.
+//   NN: B = B[K,N] row-major (ldb = N) — BASELINE.json's layout.  The LDS tile is
+//        stored as loaded, [BK][BN], and the K-contiguous MFMA operand is formed
+//        by ds_read_b64_tr_b16 (gfx950 transpose read): within a 16-lane group,
+//        lane l receives element (l % 4) of the 8-byte chunks addressed by lanes
+//        4e + l/4, e = 0..3.
 // Output: f32 or bf16 (round to nearest even), optional bias / bias+ReLU.
 // Split-K: partition p covers K range [p*Kp, (p+1)*Kp) and writes its own f32
-// plane at Y + p*y_split_stride (src/t0/gemm_gen.rs:760-793), or, with
-// reduce_ws != 0, an f32 plane in a workspace that a reduce kernel sums.
+// plane at Y + p*y_split_stride (src/t0/gemm_gen.rs:760-793).
 #pragma once
 #include <hip/hip_runtime.h>
 #include <stdint.h>
@@ -29,6 +38,7 @@ typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+typedef short i16x4 __attribute__((ext_vector_type(4)));
 
 enum : uint32_t { EPI_NONE = 0, EPI_BIAS = 1, EPI_BIAS_RELU = 2 };
 
@@ -55,15 +65,20 @@ __device__ __forceinline__ uint16_t f32_to_bf16_rne(float f) {
   return __builtin_bit_cast(uint16_t, h);
 }
 
-// XOR swizzle of 16-byte chunks inside an LDS row of KC chunks.  Any 8
-// consecutive rows (aligned to 8) reading the same logical chunk land in 8
-// distinct 16-byte slots of a 128-byte bank line, and the 8x8-transposed NN
-// stores (rows 8*nb + i, i fixed) also spread over the slots.
+// XOR swizzle of 16-byte chunks inside a K-contiguous LDS row of KC chunks.
+// Any 8 consecutive rows (aligned to 8) reading the same logical chunk land in
+// 8 distinct 16-byte slots of a 128-byte bank line.
+// Only the low 5 row bits are used, so rows 32 apart share the swizzle.
 template <int KC>
 __device__ __forceinline__ int swz(int r) {
   constexpr int RPL = 8 / KC;  // rows per 128-byte line
-  return ((r / RPL) ^ (r >> 3)) & (KC - 1);
+  return ((r / RPL) ^ ((r >> 3) & 3)) & (KC - 1);
 }
+
+// Swizzle of the 16-byte chunks of an NN B row (row = k).  The transpose read
+// of a 16-lane group touches 4 consecutive rows, 32 bytes each (chunks 2m,
+// 2m+1); XOR with 2*(k % 4) puts the 4 rows in distinct 32-byte slots.
+__device__ __forceinline__ int swz_nn(int k) { return (k & 3) << 1; }
 
 // Linear workgroup id -> (tile_m, tile_n, partition).
 // Workgroups are dispatched round-robin over the 8 XCDs; with xcd_remap the
@@ -87,26 +102,76 @@ __device__ __forceinline__ void tile_coords(const GemmParams& p, int& tm, int& t
   tn = (int)(r / gm);
 }
 
-template <int BM, int BN, int BK, int WM, int WN, bool NN>
-__global__ __launch_bounds__(WM * WN * 64) void gemm_bf16_kernel(GemmParams p) {
-  constexpr int NTHR = WM * WN * 64;
-  constexpr int TM = BM / WM, TN = BN / WN;  // per-wave tile
-  constexpr int FM = TM / 32, FN = TN / 32;  // 32x32 MFMA blocks per wave
-  constexpr int KC = BK / 8;                 // 16-byte chunks per LDS row
-  constexpr int KS = BK / 16;                // MFMA k-steps per tile
+// 16-byte global -> LDS DMA: lane i's 16 bytes land at LDS byte address
+// m0 + 16*i.  Issued through inline asm so the compiler does not track it; the
+// kernel waits for it explicitly (vmcnt + barrier) before the stage is read.
+// No "memory" clobber: the DMA always targets a stage that no instruction
+// between two barriers reads, so LDS reads may be scheduled across it; being
+// volatile, it keeps its order against the barrier and waitcnt builtins.
+__device__ __forceinline__ void lds_dma16(const void* g, uint32_t lds_byte_addr) {
+  const uint32_t m0v = __builtin_amdgcn_readfirstlane(lds_byte_addr);
+  uint32_t saved;
+  // m0 is a compiler-reserved register: keep its value across the statement.
+  asm volatile(
+      "s_mov_b32 %0, m0\n\t"
+      "s_mov_b32 m0, %2\n\t"
+      "global_load_lds_dwordx4 %1, off\n\t"
+      "s_mov_b32 m0, %0"
+      : "=&s"(saved)
+      : "v"(g), "s"(m0v)
+      :);
+}
+
+__device__ __forceinline__ uint32_t lds_addr(const void* p) {
+  return (uint32_t)(size_t)(const __attribute__((address_space(3))) void*)p;
+}
+
+// s_waitcnt vmcnt(N) (gfx9 encoding: vmcnt low bits [3:0], high bits [15:14];
+// expcnt and lgkmcnt left at their maxima).
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N <= 63, "vmcnt is 6 bits");
+  __builtin_amdgcn_s_waitcnt((N & 0xF) | ((N >> 4) << 14) | (0x7 << 4) | (0xF << 8));
+}
+
+// 16 zero bytes: the DMA source of K-tail chunks, so every K tile issues the
+// same number of DMA loads (the vmcnt arithmetic below relies on it).
+static __device__ __attribute__((aligned(16))) const uint32_t g_zero16[4] = {0u, 0u, 0u, 0u};
+
+template <int BM, int BN, int BK, int WM, int WN, int S, bool NN>
+struct GemmTile {
+  static constexpr int NWAVES = WM * WN;
+  static constexpr int NTHR = NWAVES * 64;
+  static constexpr int TM = BM / WM, TN = BN / WN;  // per-wave tile
+  static constexpr int FM = TM / 32, FN = TN / 32;  // 32x32 MFMA blocks per wave
+  static constexpr int KC = BK / 8;                 // 16-byte chunks per K-contiguous row
+  static constexpr int KS = BK / 16;                // MFMA k-steps per tile
+  static constexpr int NC = BN / 8;                 // NN: 16-byte chunks per B row
+  static constexpr int A_ELEMS = BM * BK, B_ELEMS = BN * BK;
+  static constexpr int A_BLOCKS = A_ELEMS * 2 / 1024;  // 1 KB LDS blocks per A tile
+  static constexpr int B_BLOCKS = B_ELEMS * 2 / 1024;
   static_assert(TM % 32 == 0 && TN % 32 == 0, "wave tile must be a multiple of 32x32");
   static_assert(BK == 16 || BK == 32 || BK == 64, "tile_k must be 16, 32 or 64");
-  constexpr int A_CH = BM * KC;                    // 16-byte chunks of the A tile
-  constexpr int A_LD = (A_CH + NTHR - 1) / NTHR;   // per thread
-  constexpr int B_CH = BN * KC;                    // NT: chunks of the B tile
-  constexpr int B_LD = (B_CH + NTHR - 1) / NTHR;
-  constexpr int B_BLK = (BK / 8) * (BN / 8);       // NN: 8x8 blocks of the B tile
-  constexpr int B_BL = (B_BLK + NTHR - 1) / NTHR;
-  constexpr int A_ELEMS = BM * BK, B_ELEMS = BN * BK;
+  static_assert((A_ELEMS * 2) % 1024 == 0 && (B_ELEMS * 2) % 1024 == 0, "tiles must be whole 1 KB blocks");
+  static_assert(!NN || NC >= 8, "NN tiles need tile_n >= 64");
+  static_assert(S >= 2 && S <= 5, "2..5 LDS stages");
+  // With more than two stages a wave waits for its oldest tile by count, so
+  // every wave must issue the same number of DMA loads per tile.
+  static_assert(S == 2 || (A_BLOCKS % NWAVES == 0 && B_BLOCKS % NWAVES == 0), "uneven DMA split");
+  static constexpr int LPT = A_BLOCKS / NWAVES + B_BLOCKS / NWAVES;  // DMA loads per wave per tile
+  static_assert(S == 2 || LPT * (S - 2) <= 63, "vmcnt range");
+  static_assert(S == 2 || KS % 2 == 0, "cross-tile fragment prefetch needs an even number of k-steps");
+};
 
-  __shared__ __attribute__((aligned(16))) uint16_t smem[2 * (A_ELEMS + B_ELEMS)];
-  uint16_t* const As0 = smem;
-  uint16_t* const Bs0 = smem + 2 * A_ELEMS;
+template <int BM, int BN, int BK, int WM, int WN, int S, bool NN>
+__global__ __launch_bounds__(WM * WN * 64) void gemm_bf16_kernel(GemmParams p) {
+  using T = GemmTile<BM, BN, BK, WM, WN, S, NN>;
+  constexpr int FM = T::FM, FN = T::FN, KC = T::KC, KS = T::KS, NC = T::NC;
+  constexpr int TM = T::TM, TN = T::TN;
+  constexpr int A_ELEMS = T::A_ELEMS, B_ELEMS = T::B_ELEMS;
+
+  constexpr int BUF = A_ELEMS + B_ELEMS;  // elements per LDS stage (A tile then B tile)
+  __shared__ __attribute__((aligned(1024))) uint16_t smem[S * BUF];
 
   int tm, tn, part;
   tile_coords(p, tm, tn, part);
@@ -120,94 +185,97 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_bf16_kernel(GemmParams p) {
   if (kend > (int)p.K) kend = (int)p.K;
   const int nk = kend > kbeg ? (kend - kbeg + BK - 1) / BK : 0;
 
-  u32x4 ra[A_LD];
-  u32x4 rb[NN ? B_BL * 8 : B_LD];
-
-  auto gload = [&](int k0) {
+  // ---- global -> LDS ------------------------------------------------------
+  // Wave w fills 1 KB blocks w, w + NWAVES, ...; lane l writes chunk l of its
+  // block, fetching the global chunk that the swizzle assigns to that slot.
+  const int wave_s = __builtin_amdgcn_readfirstlane(wave);
+  const uint32_t smem_base = lds_addr(smem);
+  auto load_tile = [&](int k0, int stage) {
+    const uint32_t a_lds = smem_base + (uint32_t)(stage * BUF * 2);
+    const uint32_t b_lds = a_lds + (uint32_t)(A_ELEMS * 2);
 #pragma unroll
-    for (int j = 0; j < A_LD; ++j) {
-      const int i = tid + j * NTHR;
-      const int row = i / KC, c = i % KC;
+    for (int j = 0; j < (T::A_BLOCKS + T::NWAVES - 1) / T::NWAVES; ++j) {
+      const int blk = wave_s + j * T::NWAVES;
+      if (T::A_BLOCKS % T::NWAVES != 0 && blk >= T::A_BLOCKS) break;
+      const int q = blk * 64 + lane;
+      const int row = q / KC, pc = q % KC;
+      const int lc = pc ^ swz<KC>(row);
       int gr = m0 + row;
       gr = gr < (int)p.M ? gr : (int)p.M - 1;
-      const int gk = k0 + c * 8;
-      u32x4 v = {0u, 0u, 0u, 0u};
-      if ((A_CH % NTHR == 0 || i < A_CH) && gk < kend)
-        v = *(const u32x4*)(p.a + (size_t)gr * p.lda + gk);
-      ra[j] = v;
+      const int gk = k0 + lc * 8;
+      const void* src = gk < kend ? (const void*)(p.a + (size_t)gr * p.lda + gk) : (const void*)g_zero16;
+      lds_dma16(src, a_lds + blk * 1024);
     }
-    if constexpr (!NN) {
 #pragma unroll
-      for (int j = 0; j < B_LD; ++j) {
-        const int i = tid + j * NTHR;
-        const int row = i / KC, c = i % KC;
+    for (int j = 0; j < (T::B_BLOCKS + T::NWAVES - 1) / T::NWAVES; ++j) {
+      const int blk = wave_s + j * T::NWAVES;
+      if (T::B_BLOCKS % T::NWAVES != 0 && blk >= T::B_BLOCKS) break;
+      const int q = blk * 64 + lane;
+      const void* src;
+      if constexpr (!NN) {
+        const int row = q / KC, pc = q % KC;
+        const int lc = pc ^ swz<KC>(row);
         int gr = n0 + row;
         gr = gr < (int)p.N ? gr : (int)p.N - 1;
-        const int gk = k0 + c * 8;
-        u32x4 v = {0u, 0u, 0u, 0u};
-        if ((B_CH % NTHR == 0 || i < B_CH) && gk < kend)
-          v = *(const u32x4*)(p.b + (size_t)gr * p.ldb + gk);
-        rb[j] = v;
+        const int gk = k0 + lc * 8;
+        src = gk < kend ? (const void*)(p.b + (size_t)gr * p.ldb + gk) : (const void*)g_zero16;
+      } else {
+        const int row = q / NC, pc = q % NC;  // row = k within the tile
+        const int lc = pc ^ swz_nn(row);
+        int gn = n0 + lc * 8;
+        gn = gn < (int)p.N ? gn : (int)p.N - 8;
+        const int gk = k0 + row;
+        src = gk < kend ? (const void*)(p.b + (size_t)gk * p.ldb + gn) : (const void*)g_zero16;
       }
-    } else {
-#pragma unroll
-      for (int j = 0; j < B_BL; ++j) {
-        const int bi = tid + j * NTHR;
-        const int kb = bi / (BN / 8), nb = bi % (BN / 8);
-        const int gn = n0 + nb * 8;
-        const bool ok = (B_BLK % NTHR == 0 || bi < B_BLK) && gn < (int)p.N;
-#pragma unroll
-        for (int r = 0; r < 8; ++r) {
-          const int gk = k0 + kb * 8 + r;
-          u32x4 v = {0u, 0u, 0u, 0u};
-          if (ok && gk < kend) v = *(const u32x4*)(p.b + (size_t)gk * p.ldb + gn);
-          rb[j * 8 + r] = v;
-        }
-      }
+      lds_dma16(src, b_lds + blk * 1024);
     }
   };
 
-  auto sstore = [&](int buf) {
-    uint16_t* As = As0 + buf * A_ELEMS;
-    uint16_t* Bs = Bs0 + buf * B_ELEMS;
+  // ---- LDS -> fragments ---------------------------------------------------
+  // K-contiguous tiles: the swizzle depends only on the low 5 row bits, so a
+  // fragment's address is a lane constant per k-step plus an immediate
+  // fm*32*BK (or fn*32*BK) offset.
+  const int lrow = lane & 31;
+  const int lhalf = lane >> 5;
+  int a_off[KS], b_off[KS];
 #pragma unroll
-    for (int j = 0; j < A_LD; ++j) {
-      const int i = tid + j * NTHR;
-      if (A_CH % NTHR == 0 || i < A_CH) {
-        const int row = i / KC, c = i % KC;
-        *(u32x4*)(As + row * BK + ((c ^ swz<KC>(row)) * 8)) = ra[j];
-      }
-    }
+  for (int ks = 0; ks < KS; ++ks) {
+    const int c = ks * 2 + lhalf;
+    a_off[ks] = (wm * TM + lrow) * BK + ((c ^ swz<KC>(lrow)) * 8);
+    b_off[ks] = (wn * TN + lrow) * BK + ((c ^ swz<KC>(lrow)) * 8);
+  }
+  // NN transpose read: 16-lane group g, lane i addresses row
+  // k = ks*16 + 8*(g>>1) + 4*r + (i>>2), columns col0 + 16*(g&1) + 4*(i&3) .. +3.
+  const int tg = lane >> 4, ti = lane & 15;
+  const int nn_krow0 = 8 * (tg >> 1) + (ti >> 2);       // + ks*16 + 4*r
+  const int nn_col0 = wn * TN + 16 * (tg & 1) + 4 * (ti & 3);  // + fn*32
+  const int nn_sw = swz_nn(nn_krow0);                   // (k & 3) is the same for every ks, r
+
+  auto read_frags = [&](const uint16_t* As, int ks, bf16x8* xa, bf16x8* xb) {
+    const uint16_t* Bs = As + A_ELEMS;
+#pragma unroll
+    for (int fm = 0; fm < FM; ++fm) xa[fm] = *(const bf16x8*)(As + a_off[ks] + fm * 32 * BK);
     if constexpr (!NN) {
 #pragma unroll
-      for (int j = 0; j < B_LD; ++j) {
-        const int i = tid + j * NTHR;
-        if (B_CH % NTHR == 0 || i < B_CH) {
-          const int row = i / KC, c = i % KC;
-          *(u32x4*)(Bs + row * BK + ((c ^ swz<KC>(row)) * 8)) = rb[j];
-        }
-      }
+      for (int fn = 0; fn < FN; ++fn) xb[fn] = *(const bf16x8*)(Bs + b_off[ks] + fn * 32 * BK);
     } else {
 #pragma unroll
-      for (int j = 0; j < B_BL; ++j) {
-        const int bi = tid + j * NTHR;
-        if (B_BLK % NTHR == 0 || bi < B_BLK) {
-          const int kb = bi / (BN / 8), nb = bi % (BN / 8);
-          const u32x4* in = &rb[j * 8];
+      for (int fn = 0; fn < FN; ++fn) {
+        const int col = nn_col0 + fn * 32;
+        const int eoff = (((col >> 3) ^ nn_sw) << 3) + (col & 4);
+        i16x4 v[2];
 #pragma unroll
-          for (int i = 0; i < 8; ++i) {
-            // column i of the 8x8 block: k = 0..7 from rows 0..7, packed in pairs.
-            const int d = i >> 1;
-            const uint32_t sel = (i & 1) ? 0x07060302u : 0x05040100u;
-            u32x4 o;
-            o.x = __builtin_amdgcn_perm(in[1][d], in[0][d], sel);
-            o.y = __builtin_amdgcn_perm(in[3][d], in[2][d], sel);
-            o.z = __builtin_amdgcn_perm(in[5][d], in[4][d], sel);
-            o.w = __builtin_amdgcn_perm(in[7][d], in[6][d], sel);
-            const int row = nb * 8 + i;
-            *(u32x4*)(Bs + row * BK + ((kb ^ swz<KC>(row)) * 8)) = o;
-          }
+        for (int r = 0; r < 2; ++r) {
+          const int krow = ks * 16 + 4 * r + nn_krow0;
+          v[r] = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+              (__attribute__((address_space(3))) i16x4*)(Bs + krow * BN + eoff));
         }
+        u32x4 u;
+        u.x = (uint32_t)(uint16_t)v[0].x | ((uint32_t)(uint16_t)v[0].y << 16);
+        u.y = (uint32_t)(uint16_t)v[0].z | ((uint32_t)(uint16_t)v[0].w << 16);
+        u.z = (uint32_t)(uint16_t)v[1].x | ((uint32_t)(uint16_t)v[1].y << 16);
+        u.w = (uint32_t)(uint16_t)v[1].z | ((uint32_t)(uint16_t)v[1].w << 16);
+        xb[fn] = __builtin_bit_cast(bf16x8, u);
       }
     }
   };
@@ -220,41 +288,94 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_bf16_kernel(GemmParams p) {
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc[fn][fm][r] = 0.0f;
 
-  const int lrow = lane & 31;
-  const int lhalf = lane >> 5;
-
-  if (nk > 0) {
-    gload(kbeg);
-    sstore(0);
-    __syncthreads();
-  }
-  for (int it = 0; it < nk; ++it) {
-    const int cur = it & 1;
-    if (it + 1 < nk) gload(kbeg + (it + 1) * BK);
-    const uint16_t* As = As0 + cur * A_ELEMS;
-    const uint16_t* Bs = Bs0 + cur * B_ELEMS;
+  // One K tile of MFMAs; the MFMAs of k-step ks overlap the LDS reads of ks + 1.
+  // LDS instructions per k-step: FM b128 reads of A, FN b128 (NT) or 2*FN
+  // transpose reads (NN) of B.
+  constexpr int NREAD = FM + (NN ? 2 * FN : FN);
+  constexpr int NMFMA = FM * FN;
+  auto compute_tile = [&](const uint16_t* As) {
+    bf16x8 xa[2][FM], xb[2][FN];
+    read_frags(As, 0, xa[0], xb[0]);
 #pragma unroll
     for (int ks = 0; ks < KS; ++ks) {
-      const int c = ks * 2 + lhalf;
-      bf16x8 xa[FM], xb[FN];
-#pragma unroll
-      for (int fm = 0; fm < FM; ++fm) {
-        const int row = wm * TM + fm * 32 + lrow;
-        xa[fm] = *(const bf16x8*)(As + row * BK + ((c ^ swz<KC>(row)) * 8));
-      }
-#pragma unroll
-      for (int fn = 0; fn < FN; ++fn) {
-        const int row = wn * TN + fn * 32 + lrow;
-        xb[fn] = *(const bf16x8*)(Bs + row * BK + ((c ^ swz<KC>(row)) * 8));
-      }
+      const int c = ks & 1;
+      if (ks + 1 < KS) read_frags(As, ks + 1, xa[c ^ 1], xb[c ^ 1]);
 #pragma unroll
       for (int fn = 0; fn < FN; ++fn)
 #pragma unroll
         for (int fm = 0; fm < FM; ++fm)
-          acc[fn][fm] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(xb[fn], xa[fm], acc[fn][fm], 0, 0, 0);
+          acc[fn][fm] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(xb[c][fn], xa[c][fm], acc[fn][fm], 0, 0, 0);
     }
-    if (it + 1 < nk) sstore(cur ^ 1);
+    // Instruction order for the scheduler: the reads of k-step 0, then each
+    // k-step's MFMAs with the next k-step's LDS reads slotted between them, so
+    // every fragment is requested a full k-step (NMFMA x 32 cycles) before use.
+    __builtin_amdgcn_sched_group_barrier(0x100, NREAD, 0);
+#pragma unroll
+    for (int ks = 0; ks + 1 < KS; ++ks) {
+#pragma unroll
+      for (int i = 0; i < NMFMA; ++i) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+        if (i < NREAD) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+      }
+      if (NREAD > NMFMA) __builtin_amdgcn_sched_group_barrier(0x100, NREAD - NMFMA, 0);
+    }
+    __builtin_amdgcn_sched_group_barrier(0x008, NMFMA, 0);
+  };
+  // Ring of S stages: tile t lives in stage t % S.
+  if (nk > 0) {
+#pragma unroll
+    for (int t = 0; t < S - 1; ++t)
+      if (t < nk) load_tile(kbeg + t * BK, t);
+  }
+  if constexpr (S == 2) {
+    // Iteration `it` waits for its own tile, the barrier publishes every
+    // wave's DMA and frees the stage computed in iteration it-1, which then
+    // receives tile it+1.
+    for (int it = 0; it < nk; ++it) {
+      wait_vmcnt<0>();
+      __syncthreads();
+      if (it + 1 < nk) load_tile(kbeg + (it + 1) * BK, (it + 1) & 1);
+      compute_tile(smem + (it & 1) * BUF);
+    }
+  } else if (nk > 0) {
+    // S >= 3: the barrier of iteration `it` publishes tile it+1 (its DMA was
+    // issued S-2 iterations earlier), so the last k-step of tile `it` already
+    // reads the first fragments of tile it+1 and the MFMA stream does not
+    // drain at tile boundaries.  It also frees stage (it-1) % S, which receives
+    // tile it+S-1; tiles it+2 .. it+S-2 stay in flight.
+    // Tile 0 landed (own DMA): S-2 younger tiles may stay in flight, but only
+    // if all S-1 prologue tiles were issued (short K issues fewer).
+    if (nk >= S - 1)
+      wait_vmcnt<(S > 2 ? T::LPT * (S - 2) : 0)>();
+    else
+      wait_vmcnt<0>();
     __syncthreads();
+    bf16x8 xa[2][FM], xb[2][FN];
+    read_frags(smem, 0, xa[0], xb[0]);
+    for (int it = 0; it < nk; ++it) {
+      if (it + S - 2 < nk)
+        wait_vmcnt<(S > 2 ? T::LPT * (S - 3) : 0)>();  // tile it+1 landed
+      else
+        wait_vmcnt<0>();
+      __syncthreads();
+      if (it + S - 1 < nk) load_tile(kbeg + (it + S - 1) * BK, (it + S - 1) % S);
+      const uint16_t* cur = smem + (it % S) * BUF;
+      const uint16_t* nxt = smem + ((it + 1) % S) * BUF;
+      const bool more = it + 1 < nk;
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks) {
+        const int c = ks & 1;  // KS is even, so every tile starts in buffer 0
+        if (ks + 1 < KS)
+          read_frags(cur, ks + 1, xa[c ^ 1], xb[c ^ 1]);
+        else if (more)
+          read_frags(nxt, 0, xa[c ^ 1], xb[c ^ 1]);
+#pragma unroll
+        for (int fn = 0; fn < FN; ++fn)
+#pragma unroll
+          for (int fm = 0; fm < FM; ++fm)
+            acc[fn][fm] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(xb[c][fn], xa[c][fm], acc[fn][fm], 0, 0, 0);
+      }
+    }
   }
 
   // Epilogue.  Lane l of block (fn, fm) holds C[m][n] for
@@ -276,7 +397,10 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_bf16_kernel(GemmParams p) {
         float v0 = acc[fn][fm][g * 4 + 0], v1 = acc[fn][fm][g * 4 + 1];
         float v2 = acc[fn][fm][g * 4 + 2], v3 = acc[fn][fm][g * 4 + 3];
         if (!partial_plane && p.epilogue != EPI_NONE) {
-          v0 += p.bias[n]; v1 += p.bias[n + 1]; v2 += p.bias[n + 2]; v3 += p.bias[n + 3];
+          v0 += p.bias[n];
+          v1 += p.bias[n + 1];
+          v2 += p.bias[n + 2];
+          v3 += p.bias[n + 3];
           if (p.epilogue == EPI_BIAS_RELU) {
             v0 = fmaxf(v0, 0.0f); v1 = fmaxf(v1, 0.0f); v2 = fmaxf(v2, 0.0f); v3 = fmaxf(v3, 0.0f);
           }

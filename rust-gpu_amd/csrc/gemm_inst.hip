@@ -12,15 +12,17 @@
 
 namespace t0mi {
 
-#define T0MI_V(BM, BN, BK, WM, WN)                                                          \
-  static void launch_##BM##_##BN##_##BK##_##WM##_##WN(dim3 g, hipStream_t s, const GemmParams& p) { \
-    hipLaunchKernelGGL((gemm_bf16_kernel<BM, BN, BK, WM, WN, (T0MI_INST_NN != 0)>), g, dim3(WM * WN * 64), 0, s, p); \
+#define T0MI_V(BM, BN, BK, WM, WN, S)                                                                  \
+  static void launch_##BM##_##BN##_##BK##_##WM##_##WN##_##S(dim3 g, hipStream_t s, const GemmParams& p) { \
+    hipLaunchKernelGGL((gemm_bf16_kernel<BM, BN, BK, WM, WN, S, (T0MI_INST_NN != 0)>), g, dim3(WM * WN * 64), 0, s, \
+                       p);                                                                             \
   }
 #include "gemm_variants.def"
 #undef T0MI_V
 
 static const GemmLaunchEntry kTable[] = {
-#define T0MI_V(BM, BN, BK, WM, WN) {BM, BN, BK, WM, WN, T0MI_INST_NN, launch_##BM##_##BN##_##BK##_##WM##_##WN},
+#define T0MI_V(BM, BN, BK, WM, WN, S) \
+  {BM, BN, BK, WM, WN, S, T0MI_INST_NN, launch_##BM##_##BN##_##BK##_##WM##_##WN##_##S},
 #include "gemm_variants.def"
 #undef T0MI_V
 };

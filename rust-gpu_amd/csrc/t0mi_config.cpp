@@ -58,9 +58,11 @@ bool wave_layout(const t0mi_gemm_config& c, uint32_t* wm, uint32_t* wn) {
   return true;
 }
 
+uint32_t stages_of(const t0mi_gemm_config& c) { return c.stages ? c.stages : 2u; }
+
 static uint32_t lds_total(const t0mi_gemm_config& c) {
-  // Double-buffered A and B tiles, bf16, no padding (XOR swizzle instead).
-  return 2u * (c.tile_m + c.tile_n) * c.tile_k * 2u;
+  // `stages` copies of the A and B tiles, bf16, no padding (XOR swizzle instead).
+  return stages_of(c) * (c.tile_m + c.tile_n) * c.tile_k * 2u;
 }
 
 static uint32_t est_regs(const t0mi_gemm_config& c) {
@@ -86,6 +88,7 @@ bool config_feasible(const t0mi_gemm_config& c, std::string* why) {
   uint32_t wm, wn;
   if (!wave_layout(c, &wm, &wn)) return fail("no wave layout splits the tile into 32x32 multiples");
   if (c.tile_m % (32 * wm) || c.tile_n % (32 * wn)) return fail("wave tile is not a multiple of 32x32");
+  if (stages_of(c) < 2 || stages_of(c) > 5) return fail("stages must be 2..5");
   if (lds_total(c) > 160u * 1024u) return fail("LDS over 160 KB");
   if (est_regs(c) > 512) return fail("estimated registers over 512 (VGPR+AGPR)");
   const uint32_t sk = split_k_of(c);
@@ -121,8 +124,10 @@ std::string config_name(const t0mi_gemm_config& c) {
     if (!wave_layout(d, &dm, &dn) || dm != c.wave_m || dn != c.wave_n)
       snprintf(wave_tag, sizeof wave_tag, "_w%ux%u", c.wave_m, c.wave_n);
   }
-  snprintf(buf, sizeof buf, "t0_gemm_%ux%u_k%u%s%s%s%s%s%s%s%s%s", c.tile_m, c.tile_n, c.tile_k, lds_tag,
-           sk_tag, pass_tag, grid_tag, wgp_tag, trans_tag, epi_tag, out_tag, wave_tag);
+  char stage_tag[16] = "";
+  if (stages_of(c) != 2) snprintf(stage_tag, sizeof stage_tag, "_s%u", stages_of(c));
+  snprintf(buf, sizeof buf, "t0_gemm_%ux%u_k%u%s%s%s%s%s%s%s%s%s%s", c.tile_m, c.tile_n, c.tile_k, lds_tag,
+           sk_tag, pass_tag, grid_tag, wgp_tag, trans_tag, epi_tag, out_tag, wave_tag, stage_tag);
   return buf;
 }
 
@@ -132,7 +137,7 @@ const std::vector<GemmVariant>& gemm_variants() {
   static const std::vector<GemmVariant> v = [] {
     std::vector<GemmVariant> out;
     for (int nn = 0; nn < 2; ++nn) {
-#define T0MI_V(BM, BN, BK, WM, WN) out.push_back(GemmVariant{BM, BN, BK, WM, WN, nn});
+#define T0MI_V(BM, BN, BK, WM, WN, S) out.push_back(GemmVariant{BM, BN, BK, WM, WN, S, nn});
 #include "gemm_variants.def"
 #undef T0MI_V
     }
@@ -146,7 +151,8 @@ bool has_variant(const t0mi_gemm_config& c) {
   if (!wave_layout(c, &wm, &wn)) return false;
   for (const auto& v : gemm_variants())
     if ((uint32_t)v.bm == c.tile_m && (uint32_t)v.bn == c.tile_n && (uint32_t)v.bk == c.tile_k &&
-        (uint32_t)v.wm == wm && (uint32_t)v.wn == wn && (uint32_t)v.nn == (c.transpose == T0MI_NN))
+        (uint32_t)v.wm == wm && (uint32_t)v.wn == wn && (uint32_t)v.stages == stages_of(c) &&
+        (uint32_t)v.nn == (c.transpose == T0MI_NN))
       return true;
   return false;
 }
@@ -190,9 +196,10 @@ static double estimate_us(const t0mi_gemm_config& c, uint32_t m, uint32_t n, uin
 }
 
 static t0mi_gemm_config make_cfg(int bm, int bn, int bk, int wm, int wn, uint32_t sk, uint32_t transpose,
-                                 uint32_t out_dtype) {
+                                 uint32_t out_dtype, uint32_t stages = 2) {
   t0mi_gemm_config c;
   memset(&c, 0, sizeof c);
+  c.stages = stages == 2 ? 0 : stages;
   c.tile_m = bm;
   c.tile_n = bn;
   c.tile_k = bk;
@@ -223,7 +230,7 @@ std::vector<t0mi_gemm_config> rank_candidates(uint32_t m, uint32_t n, uint32_t k
     for (uint32_t sk = 1; sk <= 16; sk *= 2) {
       // Each partition keeps at least two K tiles.
       if (sk > 1 && (uint64_t)k < (uint64_t)sk * v.bk * 2) break;
-      t0mi_gemm_config c = make_cfg(v.bm, v.bn, v.bk, v.wm, v.wn, sk, transpose, out_dtype);
+      t0mi_gemm_config c = make_cfg(v.bm, v.bn, v.bk, v.wm, v.wn, sk, transpose, out_dtype, v.stages);
       if (!config_feasible(c, nullptr)) continue;
       scored.push_back({estimate_us(c, m, n, k), c});
     }
@@ -269,13 +276,16 @@ const Preset kPresets[] = {
 };
 struct Preset950 {
   const char* name;
-  int bm, bn, bk, wm, wn;
+  int bm, bn, bk, wm, wn, stages;
 };
 const Preset950 kPresets950[] = {
-    {"gfx950_256x256_k64_w2x4", 256, 256, 64, 2, 4}, {"gfx950_256x128_k64_w2x2", 256, 128, 64, 2, 2},
-    {"gfx950_128x256_k64_w2x2", 128, 256, 64, 2, 2}, {"gfx950_128x128_k64_w2x2", 128, 128, 64, 2, 2},
-    {"gfx950_128x64_k64_w2x2", 128, 64, 64, 2, 2},   {"gfx950_64x128_k64_w2x2", 64, 128, 64, 2, 2},
-    {"gfx950_64x64_k64_w2x2", 64, 64, 64, 2, 2},     {"gfx950_128x128_k32_w2x2", 128, 128, 32, 2, 2},
+    {"gfx950_256x256_k64_w2x4", 256, 256, 64, 2, 4, 2},    {"gfx950_256x256_k32_w2x4_s3", 256, 256, 32, 2, 4, 3},
+    {"gfx950_256x256_k32_w2x4_s4", 256, 256, 32, 2, 4, 4}, {"gfx950_256x256_k64_w2x2", 256, 256, 64, 2, 2, 2},
+    {"gfx950_256x128_k64_w2x4_s3", 256, 128, 64, 2, 4, 3}, {"gfx950_256x128_k64_w2x2", 256, 128, 64, 2, 2, 2},
+    {"gfx950_128x256_k64_w2x2", 128, 256, 64, 2, 2, 2},    {"gfx950_128x128_k64_w2x2", 128, 128, 64, 2, 2, 2},
+    {"gfx950_128x128_k64_w2x2_s3", 128, 128, 64, 2, 2, 3}, {"gfx950_128x64_k64_w2x2", 128, 64, 64, 2, 2, 2},
+    {"gfx950_64x128_k64_w2x2", 64, 128, 64, 2, 2, 2},      {"gfx950_64x64_k64_w2x2", 64, 64, 64, 2, 2, 2},
+    {"gfx950_128x128_k32_w2x2", 128, 128, 32, 2, 2, 2},
 };
 }  // namespace
 
@@ -298,7 +308,7 @@ extern "C" int t0mi_config_preset(const char* name, t0mi_gemm_config* out) {
   }
   for (const auto& p : kPresets950) {
     if (strcmp(p.name, name) == 0) {
-      *out = make_cfg(p.bm, p.bn, p.bk, p.wm, p.wn, 1, T0MI_NT, T0MI_OUT_F32);
+      *out = make_cfg(p.bm, p.bn, p.bk, p.wm, p.wn, 1, T0MI_NT, T0MI_OUT_F32, p.stages);
       return T0MI_OK;
     }
   }
@@ -309,6 +319,21 @@ extern "C" int t0mi_config_preset_names(char* buf, size_t len) {
   std::string s;
   for (const auto& p : kPresets) s += std::string(s.empty() ? "" : ",") + p.name;
   for (const auto& p : kPresets950) s += std::string(",") + p.name;
+  if (buf && len) {
+    strncpy(buf, s.c_str(), len - 1);
+    buf[len - 1] = 0;
+  }
+  return (int)s.size();
+}
+
+extern "C" int t0mi_gemm_variants(char* buf, size_t len) {
+  std::string s;
+  for (const auto& v : gemm_variants()) {
+    char e[64];
+    snprintf(e, sizeof e, "%s%dx%dx%d_w%dx%d_s%d%s", s.empty() ? "" : ",", v.bm, v.bn, v.bk, v.wm, v.wn, v.stages,
+             v.nn ? "_nn" : "");
+    s += e;
+  }
   if (buf && len) {
     strncpy(buf, s.c_str(), len - 1);
     buf[len - 1] = 0;

@@ -16,7 +16,7 @@ namespace t0mi {
 
 typedef void (*GemmLaunchFn)(dim3 grid, hipStream_t stream, const GemmParams& p);
 struct GemmLaunchEntry {
-  int bm, bn, bk, wm, wn, nn;
+  int bm, bn, bk, wm, wn, stages, nn;
   GemmLaunchFn fn;
 };
 // Tables defined by the gemm_inst.hip objects (one per variant block and layout).

@@ -20,8 +20,10 @@ uint32_t split_k_of(const t0mi_gemm_config& c);
 
 // Prebuilt gfx950 GEMM variants (template instantiations).
 struct GemmVariant {
-  int bm, bn, bk, wm, wn, nn;
+  int bm, bn, bk, wm, wn, stages, nn;
 };
+// LDS pipeline stages of a config (0 means the default, 2).
+uint32_t stages_of(const t0mi_gemm_config& c);
 // All prebuilt variants (both layouts).
 const std::vector<GemmVariant>& gemm_variants();
 bool has_variant(const t0mi_gemm_config& c);

@@ -31,7 +31,7 @@ const GemmLaunchEntry* find_gemm_launch(const t0mi_gemm_config& c) {
     const GemmLaunchEntry* t = tf(&n);
     for (size_t i = 0; i < n; ++i)
       if ((uint32_t)t[i].bm == c.tile_m && (uint32_t)t[i].bn == c.tile_n && (uint32_t)t[i].bk == c.tile_k &&
-          (uint32_t)t[i].wm == wm && (uint32_t)t[i].wn == wn)
+          (uint32_t)t[i].wm == wm && (uint32_t)t[i].wn == wn && (uint32_t)t[i].stages == stages_of(c))
         return &t[i];
   }
   return nullptr;
@@ -310,7 +310,7 @@ extern "C" int t0mi_kernel_get(t0mi_ctx* ctx, const t0mi_gemm_config* cfg, t0mi_
   k->cfg = *cfg;
   k->name = name;
   k->kernarg_size = cfg->epilogue == T0MI_EPI_STORE_F32 ? 40u : 48u;
-  k->lds_size = 2u * (cfg->tile_m + cfg->tile_n) * cfg->tile_k * 2u;
+  k->lds_size = t0mi_config_lds_total(cfg);
   k->wg_size = cfg->wg_size;
   k->gemm = e;
   *out = k.get();

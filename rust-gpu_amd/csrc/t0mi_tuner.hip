@@ -124,6 +124,8 @@ struct t0mi_tuner {
     parse_bool(js, "swap", &c.swap_grid);
     parse_u32(js, "wave_m", &c.wave_m);
     parse_u32(js, "wave_n", &c.wave_n);
+    parse_u32(js, "stages", &c.stages);
+    if (c.stages == 2) c.stages = 0;
     c.use_lds = 1;
     c.double_buffer = 1;
     c.transpose = std::get<3>(key);
@@ -148,9 +150,11 @@ struct t0mi_tuner {
     char head[512];
     snprintf(head, sizeof head,
              "{\"tile_m\":%u,\"tile_n\":%u,\"tile_k\":%u,\"wg_size\":%u,\"split_k\":%u,\"lds_pad\":%u,"
-             "\"n_col_passes\":%u,\"wgp\":%s,\"swap\":%s,\"wave_m\":%u,\"wave_n\":%u,\"tflops\":%.2f,\"all\":[",
+             "\"n_col_passes\":%u,\"wgp\":%s,\"swap\":%s,\"wave_m\":%u,\"wave_n\":%u,\"stages\":%u,\"tflops\":%.2f,"
+             "\"all\":[",
              c.tile_m, c.tile_n, c.tile_k, c.wg_size, split_k_of(c), c.lds_pad, c.n_col_passes,
-             c.wgp_mode ? "true" : "false", c.swap_grid ? "true" : "false", c.wave_m, c.wave_n, r.best_tflops);
+             c.wgp_mode ? "true" : "false", c.swap_grid ? "true" : "false", c.wave_m, c.wave_n, stages_of(c),
+             r.best_tflops);
     std::string js = std::string(head) + all + "]}";
     FILE* f = fopen(path(key).c_str(), "wb");
     if (!f) {

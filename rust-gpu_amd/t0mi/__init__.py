@@ -44,7 +44,8 @@ class GemmConfig(ctypes.Structure):
     """Mirror of ``GemmConfig`` (src/t0/gemm_gen.rs:55-84) plus gfx950 fields."""
     _fields_ = [(n, ctypes.c_uint32) for n in (
         "tile_m", "tile_n", "tile_k", "wg_size", "use_lds", "double_buffer", "split_k", "lds_pad",
-        "n_col_passes", "swap_grid", "wgp_mode", "transpose", "epilogue", "out_dtype", "wave_m", "wave_n")]
+        "n_col_passes", "swap_grid", "wgp_mode", "transpose", "epilogue", "out_dtype", "wave_m", "wave_n",
+        "stages")]
 
     def copy(self, **kw) -> "GemmConfig":
         c = GemmConfig()
@@ -82,6 +83,7 @@ SIGNATURES = {
     "t0mi_build_target": (_CHARP, []),
     "t0mi_config_preset": (_I, [_CHARP, _CFG]),
     "t0mi_config_preset_names": (_I, [_CHARP, _SZ]),
+    "t0mi_gemm_variants": (_I, [_CHARP, _SZ]),
     "t0mi_config_n_waves": (_U32, [_CFG]),
     "t0mi_config_lds_total": (_U32, [_CFG]),
     "t0mi_config_estimated_regs": (_U32, [_CFG]),
@@ -173,6 +175,25 @@ def preset_names() -> list:
     buf = ctypes.create_string_buffer(4096)
     lib().t0mi_config_preset_names(buf, 4096)
     return buf.value.decode().split(",")
+
+
+def variants(transpose: Optional[int] = None) -> list:
+    """Configs of every prebuilt gfx950 GEMM kernel (optionally one layout)."""
+    buf = ctypes.create_string_buffer(16384)
+    lib().t0mi_gemm_variants(buf, 16384)
+    out = []
+    for e in buf.value.decode().split(","):
+        nn = e.endswith("_nn")
+        tile, wave, st = e.replace("_nn", "").replace("_s", "_w").split("_w")
+        bm, bn, bk = map(int, tile.split("x"))
+        wm, wn = map(int, wave.split("x"))
+        if transpose is not None and transpose != (NN if nn else NT):
+            continue
+        c = GemmConfig(tile_m=bm, tile_n=bn, tile_k=bk, wg_size=64 * wm * wn, use_lds=1, double_buffer=1,
+                       n_col_passes=1, swap_grid=1, transpose=NN if nn else NT, wave_m=wm, wave_n=wn,
+                       stages=0 if int(st) == 2 else int(st))
+        out.append(c)
+    return out
 
 
 def config_name(cfg: GemmConfig) -> str:
