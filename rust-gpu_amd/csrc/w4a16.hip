@@ -193,6 +193,120 @@ __global__ __launch_bounds__(WAVES * 64) void w4a16_decode_kernel(W4Params p) {
   }
 }
 
+// Decode kernel for group sizes of KBPG k-blocks (32 K values each) with
+// KBPG | KBW: every wave covers whole groups, so group boundaries are static.
+// Same decomposition as w4a16_decode_kernel (one 64-column strip per
+// workgroup, waves split the K range, LDS reduction in wave order), but the
+// weights, activations, scales and zero points of the wave are all requested
+// up front, out-of-range k-blocks are zero-filled instead of branched around,
+// and the loop over groups is fully static.
+template <int WAVES, int KBW, int KBPG, bool ZEROS>
+__global__ __launch_bounds__(WAVES * 64) void w4a16_decode_grouped(W4Params p) {
+  static_assert(KBW % KBPG == 0, "whole groups per wave");
+  constexpr int NG = KBW / KBPG;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int c = lane & 15, g = lane >> 4;
+  const int n0 = blockIdx.x * 64;
+  const int ncol = n0 + 4 * c;
+  const int kb_tot = (int)(p.K / 32);
+  const int kb0 = (int)(blockIdx.y * p.kb_per_split) + wave * KBW;
+  const bool col_ok = ncol < (int)p.N;
+  const int ncol_c = col_ok ? ncol : 0;
+  const bool row_ok = c < (int)p.M;
+  const int ngroups = kb_tot / KBPG;
+
+  u32x4 wv[KBW], av[KBW];
+#pragma unroll
+  for (int b = 0; b < KBW; ++b) {
+    const int kb = kb0 + b;
+    const bool ok = kb < kb_tot;
+    const int kbc = ok ? kb : 0;
+    u32x4 w = __builtin_nontemporal_load((const u32x4*)(p.w + (size_t)(kbc * 4 + g) * p.N + ncol_c));
+    u32x4 a = *(const u32x4*)(p.a + (size_t)(row_ok ? c : 0) * p.K + kbc * 32 + g * 8);
+    wv[b] = (ok && col_ok) ? w : (u32x4){0u, 0u, 0u, 0u};
+    av[b] = (ok && row_ok) ? a : (u32x4){0u, 0u, 0u, 0u};
+  }
+  u32x2 sv[NG];
+  uint32_t zv[NG];
+#pragma unroll
+  for (int q = 0; q < NG; ++q) {
+    int grp = kb0 / KBPG + q;
+    grp = grp < ngroups ? grp : ngroups - 1;
+    sv[q] = *(const u32x2*)(p.scales + (size_t)grp * p.N + ncol_c);
+    zv[q] = ZEROS ? p.zeros[(size_t)grp * (p.N / 8) + ncol_c / 8] >> (4 * (ncol_c & 7)) : 0u;
+  }
+
+  const bf16x8_t ones = __builtin_bit_cast(bf16x8_t, (u32x4){0x3F803F80u, 0x3F803F80u, 0x3F803F80u, 0x3F803F80u});
+  f32x4 acc[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) acc[j] = (f32x4){0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int q = 0; q < NG; ++q) {
+    f32x4 P[4], S = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int j = 0; j < 4; ++j) P[j] = (f32x4){0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int i = 0; i < KBPG; ++i) {
+      const int b = q * KBPG + i;
+      const bf16x8_t A = perm_act(av[b]);
+      S = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A, ones, S, 0, 0, 0);
+      P[0] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A, nib_pairs(wv[b].x), P[0], 0, 0, 0);
+      P[1] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A, nib_pairs(wv[b].y), P[1], 0, 0, 0);
+      P[2] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A, nib_pairs(wv[b].z), P[2], 0, 0, 0);
+      P[3] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A, nib_pairs(wv[b].w), P[3], 0, 0, 0);
+    }
+    // y += s * (P - (128 + z) * S) for the four columns ncol + j of this lane.
+    const float s4[4] = {bf16f(sv[q].x & 0xFFFFu), bf16f(sv[q].x >> 16), bf16f(sv[q].y & 0xFFFFu),
+                         bf16f(sv[q].y >> 16)};
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const float z = 128.0f + (float)(ZEROS ? ((zv[q] >> (4 * j)) & 0xFu) : p.zp_const);
+      acc[j].x = fmaf(s4[j], fmaf(-z, S.x, P[j].x), acc[j].x);
+      acc[j].y = fmaf(s4[j], fmaf(-z, S.y, P[j].y), acc[j].y);
+      acc[j].z = fmaf(s4[j], fmaf(-z, S.z, P[j].z), acc[j].z);
+      acc[j].w = fmaf(s4[j], fmaf(-z, S.w, P[j].w), acc[j].w);
+    }
+  }
+
+  // Cross-wave reduction in wave order, then store (or an f32 partial plane).
+  __shared__ float red[WAVES * 64 * 16];
+  float* mine = red + (wave * 64 + lane) * 16;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) *(f32x4*)(mine + 4 * j) = acc[j];
+  __syncthreads();
+  for (int t = threadIdx.x; t < 64 * 4; t += WAVES * 64) {
+    const int L = t >> 2, j = t & 3;
+    f32x4 s4 = *(const f32x4*)(red + L * 16 + 4 * j);
+    for (int v = 1; v < WAVES; ++v) {
+      const f32x4 t4 = *(const f32x4*)(red + (v * 64 + L) * 16 + 4 * j);
+      s4.x += t4.x;
+      s4.y += t4.y;
+      s4.z += t4.z;
+      s4.w += t4.w;
+    }
+    const int col = n0 + 4 * (L & 15) + j;
+    const int row0 = 4 * (L >> 4);
+    if (col >= (int)p.N) continue;
+    const float vals[4] = {s4.x, s4.y, s4.z, s4.w};
+    if (gridDim.y > 1) {
+      float* yp = (float*)((char*)p.y + (size_t)blockIdx.y * p.y_split_stride);
+#pragma unroll
+      for (int r = 0; r < 4; ++r)
+        if (row0 + r < (int)p.M) yp[(size_t)(row0 + r) * p.N + col] = vals[r];
+    } else if (p.out_bf16) {
+      uint16_t* yp = (uint16_t*)p.y;
+#pragma unroll
+      for (int r = 0; r < 4; ++r)
+        if (row0 + r < (int)p.M) yp[(size_t)(row0 + r) * p.N + col] = f32_to_bf16_rne(vals[r]);
+    } else {
+      float* yp = (float*)p.y;
+#pragma unroll
+      for (int r = 0; r < 4; ++r)
+        if (row0 + r < (int)p.M) yp[(size_t)(row0 + r) * p.N + col] = vals[r];
+    }
+  }
+}
+
 // Standalone dequant (replaces build_dequant_int4_{f32,bf16}, quant_kernels.rs:53-171):
 // one thread per packed word -> 8 outputs down column n.  round_mode 0: f32,
 // 1: bf16 truncation (the reference's store_bf16), 2: bf16 RNE.
@@ -275,7 +389,25 @@ extern "C" int t0mi_w4a16_gemm(t0mi_ctx* ctx, uint64_t a, uint64_t qweight, uint
     } else {
       p.y = (char*)y + (size_t)r0 * n * ob;
     }
-    hipLaunchKernelGGL((w4a16_decode_kernel<WAVES, KBW>), dim3(strips, ky), dim3(WAVES * 64), 0, ctx->stream, p);
+    const dim3 grid(strips, ky), block(WAVES * 64);
+    const bool z = qzeros != 0;
+    switch (group) {
+#define T0MI_W4_CASE(G)                                                                                    \
+  case G:                                                                                                  \
+    if (z)                                                                                                 \
+      hipLaunchKernelGGL((w4a16_decode_grouped<WAVES, KBW, G / 32, true>), grid, block, 0, ctx->stream, p);  \
+    else                                                                                                   \
+      hipLaunchKernelGGL((w4a16_decode_grouped<WAVES, KBW, G / 32, false>), grid, block, 0, ctx->stream, p); \
+    break;
+      T0MI_W4_CASE(32)
+      T0MI_W4_CASE(64)
+      T0MI_W4_CASE(128)
+      T0MI_W4_CASE(256)
+      T0MI_W4_CASE(512)
+#undef T0MI_W4_CASE
+      default:  // groups spanning several waves' K ranges
+        hipLaunchKernelGGL((w4a16_decode_kernel<WAVES, KBW>), grid, block, 0, ctx->stream, p);
+    }
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return hip_fail(e, "w4a16 launch");
     if (ky > 1) {
