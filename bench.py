@@ -33,7 +33,9 @@ def parse():
     p.add_argument("--gpus", type=int, default=1)
     p.add_argument("--steps", type=int, default=50)
     p.add_argument("--warmup", type=int, default=10)
-    p.add_argument("--only", choices=["all", "gemm", "w4a16"], default="all")
+    p.add_argument("--only", choices=["all", "gemm", "w4a16", "copy"], default="all",
+                   help="'copy' runs only a plain 1 GiB fp32 copy kernel: the calibration for rocprofv3 "
+                        "FETCH_SIZE/WRITE_SIZE readings")
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     p.add_argument("--config", default=None, help="GEMM preset name to force (default: auto_select)")
     return p.parse_args()
@@ -153,15 +155,40 @@ def cpu_baseline(which):
                       f"then the sequential-fp32 loop"}
 
 
+def copy_calibration(args, torch):
+    """A plain elementwise copy of known size (1 GiB read + 1 GiB written per launch).  Under
+    rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE its readings give the counters' scale factor."""
+    n = 1 << 28
+    x = torch.ones(n, device="cuda:0", dtype=torch.float32)
+    y = torch.empty_like(x)
+    for _ in range(max(1, args.warmup)):
+        torch.add(x, 1.0, out=y)
+    torch.cuda.synchronize()
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(args.steps):
+        torch.add(x, 1.0, out=y)
+    e1.record()
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / args.steps
+    nbytes = 2 * 4 * n
+    print(json.dumps({"calibration": "fp32 copy y = x + 1", "read_bytes": 4 * n, "write_bytes": 4 * n,
+                      "ms_per_launch": round(ms, 4), "GB/s": round(nbytes / (ms * 1e-3) / 1e9, 1)}), flush=True)
+
+
 def main():
     args = parse()
     if args.gpus != 1:
-        print(f"bench.py: this build runs on one GPU only (asked for --gpus {args.gpus}); multi-GPU "
-              f"sharding of the GEMM path is described in DESIGN.md but not built.", file=sys.stderr)
+        print(f"bench.py: this build runs on one GPU only (asked for --gpus {args.gpus}); the GEMM path "
+              f"is not sharded across GPUs here.", file=sys.stderr)
         sys.exit(2)
     import torch
-    import t0mi
     torch.cuda.init()
+    if args.only == "copy":
+        copy_calibration(args, torch)
+        return
+    import t0mi
     rt = t0mi.Runtime.on_torch_stream(0)
     out = {"metric": METRIC, "n_gpus": 1, "steps": args.steps, "warmup": args.warmup, "higher_is_better": True,
            "scaling": "weak", "vs_baseline": None, "dtype": "bf16", "data": "synthetic"}

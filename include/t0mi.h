@@ -192,6 +192,103 @@ int t0mi_wait_idle(t0mi_ctx* ctx);
 int t0mi_gemm(t0mi_ctx* ctx, const t0mi_gemm_config* cfg, uint64_t x, uint64_t b, uint64_t y,
               uint64_t bias, uint32_t m, uint32_t n, uint32_t k);
 
+/* ---- tile_ir surface: TileGemm (src/t0/tile_ir.rs:100-152) ---------------- */
+/* EpilogueOp of the tile_ir fusion chain (tile_ir.rs:40-58), applied in order
+ * to every fp32 result before the store (lowered at tile_ir.rs:3400-3540):
+ *   BIAS_ADD  v += bias[col]  (bias: [N] f32)     SCALE  v *= scale
+ *   RELU      max(v, 0)                           SILU   v * rcp(1 + exp2(-v log2e))
+ *   GELU      v * rcp(1 + exp2(-1.702 v log2e))   (the sigmoid form the reference
+ *             lowers, tile_ir.rs:3470-3500, not the tanh form its doc comment names)
+ *   ABS |v|   NEG -v   CLAMP min(max(v, clamp_min), clamp_max) */
+typedef enum {
+  T0MI_TEPI_BIAS_ADD = 0,
+  T0MI_TEPI_SCALE = 1,
+  T0MI_TEPI_RELU = 2,
+  T0MI_TEPI_SILU = 3,
+  T0MI_TEPI_GELU = 4,
+  T0MI_TEPI_ABS = 5,
+  T0MI_TEPI_NEG = 6,
+  T0MI_TEPI_CLAMP = 7
+} t0mi_tile_epilogue_op;
+#define T0MI_TILE_MAX_EPILOGUE 8
+
+/* TileGemm, field for field (booleans as 0/1; waves_per_wg 0 = None), plus
+ * out_dtype.  wmma_format must be 0 (BF16_F32): the only format on this path.
+ * On gfx950 the RDNA-specific fields (wgp_mode, acc_swap, waves_per_wg) keep
+ * their meaning for name() and the grid/LDS arithmetic but do not change the
+ * kernel; triple_buffer selects a 3-stage LDS ring where one is prebuilt. */
+typedef struct t0mi_tile_spec {
+  uint32_t tile_m, tile_n, tile_k;
+  uint32_t wgp_mode, double_buffer, triple_buffer;
+  uint32_t split_k;
+  uint32_t swap_grid;
+  uint32_t transpose; /* t0mi_transpose */
+  uint32_t acc_swap;
+  uint32_t n_epilogue;
+  uint32_t epilogue[T0MI_TILE_MAX_EPILOGUE]; /* t0mi_tile_epilogue_op */
+  uint32_t persistent;
+  uint32_t waves_per_wg;
+  uint32_t wmma_format;
+  uint32_t out_dtype; /* new: T0MI_OUT_F32 (reference) or T0MI_OUT_BF16 */
+} t0mi_tile_spec;
+
+/* TileGemm::tile_* presets by function name, e.g. "tile_128x64_k16",
+ * "tile_persistent_decode" (tile_ir.rs:156-604); T0MI_ERR_NOT_FOUND if unknown. */
+int t0mi_tile_preset(const char* name, t0mi_tile_spec* out);
+/* Comma-separated preset names. */
+const char* t0mi_tile_preset_names(void);
+/* TileGemm::name (tile_ir.rs:677-701); returns the length, writes at most len-1. */
+int t0mi_tile_name(const t0mi_tile_spec* s, char* buf, size_t len);
+/* n_waves / wg_size / lds_total (tile_ir.rs:607-653), the reference's arithmetic
+ * (wave32 work-items, acc-swap region, +16 B persistent slot). */
+uint32_t t0mi_tile_n_waves(const t0mi_tile_spec* s);
+uint32_t t0mi_tile_wg_size(const t0mi_tile_spec* s);
+uint32_t t0mi_tile_lds_total(const t0mi_tile_spec* s);
+/* tile_auto_select(m, k, n, transpose) (tile_ir.rs:740-870): the reference's
+ * shape rules, including its 64 KB LDS fallback and auto split-K disabled. */
+int t0mi_tile_auto_select(uint32_t m, uint32_t k, uint32_t n, uint32_t transpose, t0mi_tile_spec* out);
+/* Kernarg bytes the lowered kernel declares: 44 (64 when persistent), then the
+ * epilogue arguments in declaration order with the reference's allocator
+ * alignment (compile.rs:120-180): bias u64 (8-aligned), scale f32, clamp_min
+ * f32, clamp_max f32 — each only when the chain uses it. */
+uint32_t t0mi_tile_kernarg_size(const t0mi_tile_spec* s);
+/* build_kernargs (tile_ir.rs:4570-4593): 44 B with the M slot left 0, and
+ * build_kernargs_m (:4595-4602): 44 B with M.  Layout [X u64 @0, WT u64 @8,
+ * Y u64 @16, K @24, N @28, split_k_shift @32, y_split_stride @36 (0), M @40].
+ * Return the byte count written (or needed, if cap is too small: nothing is
+ * written then). */
+int t0mi_tile_build_kernargs(uint64_t x, uint64_t wt, uint64_t y, uint32_t k, uint32_t n,
+                             const t0mi_tile_spec* s, uint8_t* out, size_t cap);
+int t0mi_tile_build_kernargs_m(uint64_t x, uint64_t wt, uint64_t y, uint32_t k, uint32_t n, uint32_t m,
+                               const t0mi_tile_spec* s, uint8_t* out, size_t cap);
+/* build_kernargs_m_with_counter (tile_ir.rs:4604-4637): persistent specs append
+ * counter u64 @48, n_tiles_n_shift @56, tiles_per_wg @60 (64 B). */
+int t0mi_tile_build_kernargs_m_with_counter(uint64_t x, uint64_t wt, uint64_t y, uint32_t k, uint32_t n,
+                                            uint32_t m, const t0mi_tile_spec* s, uint64_t counter,
+                                            uint32_t n_tiles_n_shift, uint32_t tiles_per_wg, uint8_t* out,
+                                            size_t cap);
+/* Appends the epilogue arguments the spec's chain declares to a kernarg buffer
+ * of *len bytes (what a reference caller writes after build_kernargs_m, per
+ * lower_gemm's declarations at tile_ir.rs:1014-1027).  Updates *len. */
+int t0mi_tile_append_epilogue_args(const t0mi_tile_spec* s, uint64_t bias, float scale, float clamp_min,
+                                   float clamp_max, uint8_t* buf, size_t cap, size_t* len);
+/* compute_grid (tile_ir.rs:4645-4666): work-items, [wg_size, 1, 1] when persistent. */
+int t0mi_tile_compute_grid(const t0mi_tile_spec* s, uint32_t m, uint32_t n, uint32_t grid_workitems[3]);
+/* lower_gemm + T0Kernel::compile + GpuKernel::load for a TileGemm
+ * (tile_ir.rs:887; compile.rs:1398): looks up the prebuilt gfx950 kernel with
+ * the spec's tile_m x tile_n x tile_k.  The handle dispatches with the spec's
+ * own kernarg layout and grid; M comes from the kernarg (0 = derive it from the
+ * grid, padded as gemm_gen does), and a persistent spec's one-WG grid launches
+ * the full tile grid (same results).  T0MI_ERR_NO_KERNEL for shapes with no
+ * gfx950 kernel (tile_k 48; NN with tile_n < 64). */
+int t0mi_tile_kernel_get(t0mi_ctx* ctx, const t0mi_tile_spec* s, t0mi_kernel** out);
+/* One-call tile GEMM: Y[m,n] = epilogue(X[m,k] . B) for the spec's transpose,
+ * with the chain's arguments; split_k > 1 is reduced deterministically (the
+ * reference's tile_ir split-K writes every partition to one plane,
+ * tile_ir.rs:4577-4581; here the sum is correct).  Asynchronous. */
+int t0mi_tile_gemm(t0mi_ctx* ctx, const t0mi_tile_spec* s, uint64_t x, uint64_t wt, uint64_t y, uint32_t m,
+                   uint32_t n, uint32_t k, uint64_t bias, float scale, float clamp_min, float clamp_max);
+
 /* ---- autotuner: GemmTuner (src/t0/auto_gemm.rs:46-527) -------------------- */
 typedef struct t0mi_tuner t0mi_tuner;
 /* GemmTuner::new (default cache dir $HOME/.t0mi_autotune_gfx950, kept apart

@@ -78,6 +78,8 @@ def lib():
         L.orc_w4a16_gemm.argtypes = [P, P, P, P, ctypes.c_int, P, i64, i64, i64, i64, ctypes.c_int]
         L.orc_w4a16_gemm.restype = ctypes.c_int
         L.orc_num_threads.restype = ctypes.c_int
+        L.orc_epilogue.argtypes = [P, i64, i64, P, ctypes.c_int, P, ctypes.c_float, ctypes.c_float,
+                                   ctypes.c_float]
         _lib = L
     return _lib
 
@@ -246,6 +248,21 @@ def w4a16_gemm(a: np.ndarray, w: np.ndarray, scales: np.ndarray, zeros, group: i
     if rc != 0:
         raise MemoryError("oracle w4a16: allocation failed")
     return y
+
+
+def epilogue(y: np.ndarray, ops, bias=None, scale: float = 1.0, clamp_min: float = 0.0,
+             clamp_max: float = 0.0) -> np.ndarray:
+    """tile_ir EpilogueOp chain (src/t0/tile_ir.rs:3400-3540) applied in order to fp32 y[M, N];
+    ops are 0..7 = bias, scale, relu, silu, gelu, abs, neg, clamp.  Returns a new array."""
+    out = np.ascontiguousarray(y, dtype=np.float32).copy()
+    M, N = out.shape
+    o = np.ascontiguousarray(list(ops), dtype=np.uint32)
+    b = None if bias is None else np.ascontiguousarray(bias, dtype=np.float32)
+    if 0 in list(ops) and (b is None or b.shape != (N,)):
+        raise ValueError("bias op needs a [N] float32 bias")
+    lib().orc_epilogue(_p(out), M, N, _p(o) if o.size else None, int(o.size), None if b is None else _p(b),
+                       scale, clamp_min, clamp_max)
+    return out
 
 
 def num_threads() -> int:

@@ -16,7 +16,10 @@
  *   - GEMM: the reference's committed torch fixtures (benchmarks/torch_ref),
  *     the integer-pattern known answers of src/t0/auto_gemm.rs:235-269,
  *     brute force against float64 on tiny shapes;
- *   - INT4: the host unit tests of src/t0/quant_kernels.rs:342-490.
+ *   - INT4: the host unit tests of src/t0/quant_kernels.rs:342-490;
+ *   - epilogue chain: closed forms per op (relu/abs/neg/clamp/scale/bias exact,
+ *     silu(0) = 0, silu(x) -> x and -> 0 in the tails, sigmoid-gelu at known
+ *     points) and order-of-application checks.
  */
 #include <stdint.h>
 #include <stdlib.h>
@@ -299,6 +302,35 @@ int orc_w4a16_gemm(const uint16_t* a, const uint32_t* w, const uint16_t* scales,
 #endif
   free(wf);
   return 0;
+}
+
+/* ------------------------------------------------------------------------ */
+/* Epilogue chain (EpilogueOp, src/t0/tile_ir.rs:40-58, lowered at 3400-3540) */
+/* ------------------------------------------------------------------------ */
+/* ops[i] in 0..7 = BiasAdd, Scale, ReLU, SiLU, GELU, Abs, Neg, Clamp, applied
+ * in order to every y[m][n] (fp32).  SiLU is x * 1/(1 + e^-x); GELU is the
+ * sigmoid form the reference lowers (tile_ir.rs:3470-3500): x * 1/(1 + e^-1.702x).
+ * Exact libm exp and division here; the GPU uses the hardware exp2 / rcp, as
+ * the reference's v_exp_f32 / v_rcp_f32 do. */
+void orc_epilogue(float* y, int64_t M, int64_t N, const uint32_t* ops, int n_ops, const float* bias,
+                  float scale, float lo, float hi) {
+  for (int64_t m = 0; m < M; ++m)
+    for (int64_t n = 0; n < N; ++n) {
+      float v = y[m * N + n];
+      for (int i = 0; i < n_ops; ++i) {
+        switch (ops[i]) {
+          case 0: v = v + bias[n]; break;
+          case 1: v = v * scale; break;
+          case 2: v = v > 0.0f ? v : 0.0f; break;
+          case 3: v = v / (1.0f + expf(-v)); break;
+          case 4: v = v / (1.0f + expf(-1.702f * v)); break;
+          case 5: v = fabsf(v); break;
+          case 6: v = -v; break;
+          default: v = v < lo ? lo : v; v = v > hi ? hi : v; break;
+        }
+      }
+      y[m * N + n] = v;
+    }
 }
 
 int orc_num_threads(void) {

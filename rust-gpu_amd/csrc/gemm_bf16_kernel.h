@@ -9,8 +9,10 @@
 //     each wave instruction fills one contiguous 1 KB LDS block, so the LDS
 //     swizzle is applied on the global side (each lane fetches the chunk that
 //     belongs at its LDS slot);
-//   * double-buffered LDS tiles, one barrier per K tile, the next tile's loads
-//     issued before the current tile's MFMAs;
+//   * a ring of S = 2..5 LDS stages, one barrier per K tile: tile it+S-1 is
+//     requested before tile it's MFMAs, and waits count outstanding DMA
+//     instructions (vmcnt) so up to S-1 tiles are in flight; with S >= 3 the
+//     first fragments of tile it+1 are read during tile it's last k-step;
 //   * v_mfma_f32_32x32x16_bf16 with the A and B fragments of the next k-step
 //     read from LDS while the current k-step's MFMAs run.
 //
@@ -24,12 +26,14 @@
 //        by ds_read_b64_tr_b16 (gfx950 transpose read): within a 16-lane group,
 //        lane l receives element (l % 4) of the 8-byte chunks addressed by lanes
 //        4e + l/4, e = 0..3.
-// Output: f32 or bf16 (round to nearest even), optional bias / bias+ReLU.
+// Output: f32 or bf16 (round to nearest even), after an optional fused epilogue chain.
 // Split-K: partition p covers K range [p*Kp, (p+1)*Kp) and writes its own f32
 // plane at Y + p*y_split_stride (src/t0/gemm_gen.rs:760-793).
 #pragma once
 #include <hip/hip_runtime.h>
 #include <stdint.h>
+
+#include "epi_chain.h"
 
 namespace t0mi {
 
@@ -40,7 +44,22 @@ typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 typedef short i16x4 __attribute__((ext_vector_type(4)));
 
-enum : uint32_t { EPI_NONE = 0, EPI_BIAS = 1, EPI_BIAS_RELU = 2 };
+__device__ __forceinline__ float epi_apply(float v, float bias, const EpiChain& e) {
+#pragma unroll 1
+  for (uint32_t i = 0; i < e.n; ++i) {
+    switch ((e.ops >> (4 * i)) & 0xFu) {
+      case EOP_BIAS: v += bias; break;
+      case EOP_SCALE: v *= e.scale; break;
+      case EOP_RELU: v = fmaxf(v, 0.0f); break;
+      case EOP_SILU: v = v * __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(-v * 1.44269504f)); break;
+      case EOP_GELU: v = v * __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(-(1.702f * v) * 1.44269504f)); break;
+      case EOP_ABS: v = fabsf(v); break;
+      case EOP_NEG: v = -v; break;
+      default: v = fminf(fmaxf(v, e.lo), e.hi); break;
+    }
+  }
+  return v;
+}
 
 struct GemmParams {
   const uint16_t* a;      // X [M,K] bf16
@@ -54,7 +73,7 @@ struct GemmParams {
   uint32_t k_per_split;   // K range per partition (multiple of 8)
   uint64_t y_split_stride;// bytes between partial planes (split_k > 1)
   uint32_t out_bf16;      // 1: bf16 RNE store, 0: f32 store
-  uint32_t epilogue;      // EPI_*
+  EpiChain epi;           // fused epilogue (final planes only)
   uint32_t swap_grid;     // reference grid axis convention (informational)
   uint32_t xcd_remap;     // 1: make tiles that share an XCD (L2) contiguous
 };
@@ -396,14 +415,13 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_bf16_kernel(GemmParams p) {
         if (n >= (int)p.N) continue;
         float v0 = acc[fn][fm][g * 4 + 0], v1 = acc[fn][fm][g * 4 + 1];
         float v2 = acc[fn][fm][g * 4 + 2], v3 = acc[fn][fm][g * 4 + 3];
-        if (!partial_plane && p.epilogue != EPI_NONE) {
-          v0 += p.bias[n];
-          v1 += p.bias[n + 1];
-          v2 += p.bias[n + 2];
-          v3 += p.bias[n + 3];
-          if (p.epilogue == EPI_BIAS_RELU) {
-            v0 = fmaxf(v0, 0.0f); v1 = fmaxf(v1, 0.0f); v2 = fmaxf(v2, 0.0f); v3 = fmaxf(v3, 0.0f);
-          }
+        if (!partial_plane && p.epi.n) {
+          f32x4 bv = {0.0f, 0.0f, 0.0f, 0.0f};
+          if (p.bias) bv = f32x4{p.bias[n], p.bias[n + 1], p.bias[n + 2], p.bias[n + 3]};
+          v0 = epi_apply(v0, bv.x, p.epi);
+          v1 = epi_apply(v1, bv.y, p.epi);
+          v2 = epi_apply(v2, bv.z, p.epi);
+          v3 = epi_apply(v3, bv.w, p.epi);
         }
         if (!partial_plane && p.out_bf16) {
           u32x2 o;

@@ -1,5 +1,5 @@
 // gemm_inst.hip — instantiates one block of gemm_variants.def for one B layout.
-// Compiled four times by the build (T0MI_PART = 0/1, T0MI_INST_NN = 0/1, with
+// Compiled six times by the build (T0MI_PART = 0/1/2, T0MI_INST_NN = 0/1, with
 // T0MI_TABLE_FN naming the table accessor) so the variants build in parallel.
 #include "t0mi_ctx.h"
 
@@ -17,6 +17,11 @@ namespace t0mi {
     hipLaunchKernelGGL((gemm_bf16_kernel<BM, BN, BK, WM, WN, S, (T0MI_INST_NN != 0)>), g, dim3(WM * WN * 64), 0, s, \
                        p);                                                                             \
   }
+#if T0MI_INST_NN
+#define T0MI_V_NT(BM, BN, BK, WM, WN, S)
+#else
+#define T0MI_V_NT(BM, BN, BK, WM, WN, S) T0MI_V(BM, BN, BK, WM, WN, S)
+#endif
 #include "gemm_variants.def"
 #undef T0MI_V
 
@@ -25,6 +30,7 @@ static const GemmLaunchEntry kTable[] = {
   {BM, BN, BK, WM, WN, S, T0MI_INST_NN, launch_##BM##_##BN##_##BK##_##WM##_##WN##_##S},
 #include "gemm_variants.def"
 #undef T0MI_V
+#undef T0MI_V_NT
 };
 
 const GemmLaunchEntry* T0MI_TABLE_FN(size_t* n) {

@@ -138,8 +138,11 @@ const std::vector<GemmVariant>& gemm_variants() {
     std::vector<GemmVariant> out;
     for (int nn = 0; nn < 2; ++nn) {
 #define T0MI_V(BM, BN, BK, WM, WN, S) out.push_back(GemmVariant{BM, BN, BK, WM, WN, S, nn});
+#define T0MI_V_NT(BM, BN, BK, WM, WN, S) \
+  if (!nn) out.push_back(GemmVariant{BM, BN, BK, WM, WN, S, nn});
 #include "gemm_variants.def"
 #undef T0MI_V
+#undef T0MI_V_NT
     }
     return out;
   }();
@@ -184,14 +187,19 @@ static double estimate_us(const t0mi_gemm_config& c, uint32_t m, uint32_t n, uin
   const double kp = ceil((double)k / sk / c.tile_k) * c.tile_k;
   const double flops_tile = 2.0 * c.tile_m * c.tile_n * kp;
   const double busy = std::min(1.0, W * wg_per_cu / 4.0);
-  const double t_comp = rounds * wg_per_cu * flops_tile / (FLOP_PER_CLK_CU * CLK * eff * busy);
+  // A single wave per SIMD has nothing to issue while it waits on its own LDS
+  // reads and barriers (measured: 256x256 with 4 waves runs ~10% slower than
+  // with 8 at 4096^3, despite the larger per-wave MFMA blocks).
+  const double hide = W * wg_per_cu / 4.0 < 2.0 ? 0.8 : 1.0;
+  const double t_comp = rounds * wg_per_cu * flops_tile / (FLOP_PER_CLK_CU * CLK * eff * busy * hide);
   const double out_b = c.out_dtype == T0MI_OUT_BF16 ? 2.0 : 4.0;
-  double hbm_bytes = 2.0 * m * k + 2.0 * k * n + out_b * m * n;
-  if (sk > 1) hbm_bytes += 2.0 * sk * 4.0 * m * n;
+  double hbm_bytes = 2.0 * m * k + 2.0 * k * n + (sk > 1 ? sk * 4.0 : out_b) * m * n;
   const double l2_bytes = tiles * (c.tile_m + c.tile_n) * kp * 2.0;
   const double t_mem = std::max(hbm_bytes / HBM, l2_bytes / L2);
   double t = std::max(t_comp, t_mem) * 1e6 + 3.0;
-  if (sk > 1) t += 3.0;  // reduce pass
+  // The split-K reduce pass is a separate launch: it reads every fp32 partial
+  // plane and writes the output once.
+  if (sk > 1) t += (sk * 4.0 + out_b) * m * n / HBM * 1e6 + 3.0;
   return t;
 }
 

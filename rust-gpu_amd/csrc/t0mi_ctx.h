@@ -24,15 +24,20 @@ const GemmLaunchEntry* gemm_table_p0_nt(size_t* n);
 const GemmLaunchEntry* gemm_table_p1_nt(size_t* n);
 const GemmLaunchEntry* gemm_table_p0_nn(size_t* n);
 const GemmLaunchEntry* gemm_table_p1_nn(size_t* n);
+const GemmLaunchEntry* gemm_table_p2_nt(size_t* n);
+const GemmLaunchEntry* gemm_table_p2_nn(size_t* n);
 const GemmLaunchEntry* find_gemm_launch(const t0mi_gemm_config& c);
 
-enum KernelKind : int { KK_GEMM_GEN = 1 };
+enum KernelKind : int { KK_GEMM_GEN = 1, KK_TILE = 2 };
 
 }  // namespace t0mi
 
 struct t0mi_kernel {
   int kind;
-  t0mi_gemm_config cfg;
+  t0mi_gemm_config cfg;       // KK_TILE: the lowered config of `tile`
+  t0mi_tile_spec tile;        // KK_TILE only
+  t0mi::TileArgLayout lay;    // KK_TILE only
+  t0mi::EpiChain chain;
   std::string name;
   uint32_t kernarg_size, lds_size, wg_size;
   const t0mi::GemmLaunchEntry* gemm;
@@ -65,7 +70,13 @@ int ensure_workspace(t0mi_ctx* ctx, size_t bytes);
 int launch_gemm(t0mi_ctx* ctx, const t0mi_gemm_config& cfg, const GemmLaunchEntry* e, GemmParams p);
 int check_ctx(t0mi_ctx* ctx);
 // Sums sk f32 planes of [M, N] (ascending plane order), applies the epilogue
-// and stores f32 or bf16 into y (row stride ldy), on ctx's stream.
+// chain and stores f32 or bf16 into y (row stride ldy), on ctx's stream.
 int launch_splitk_reduce(t0mi_ctx* ctx, const float* ws, void* y, const float* bias, uint32_t M, uint32_t N,
-                         uint32_t ldy, uint32_t sk, uint32_t out_bf16, uint32_t epilogue);
+                         uint32_t ldy, uint32_t sk, uint32_t out_bf16, const EpiChain& epi);
+// The chain of a gemm_gen EpilogueOp.
+EpiChain chain_of(uint32_t gemm_gen_epilogue);
+// Y[m,n] = epi(X . B) with a prebuilt kernel: tile-aligned or not, split-K
+// through the workspace and a deterministic reduce.  Asynchronous.
+int run_gemm(t0mi_ctx* ctx, const t0mi_gemm_config& cfg, const GemmLaunchEntry* e, uint64_t x, uint64_t b,
+             uint64_t y, uint64_t bias, uint32_t m, uint32_t n, uint32_t k, const EpiChain& epi);
 }  // namespace t0mi

@@ -6,6 +6,7 @@
 #include <vector>
 
 #include "../../include/t0mi.h"
+#include "epi_chain.h"
 
 namespace t0mi {
 
@@ -32,5 +33,22 @@ bool has_variant(const t0mi_gemm_config& c);
 // prebuilt, with split-K options.  Used by auto_select and the tuner.
 std::vector<t0mi_gemm_config> rank_candidates(uint32_t m, uint32_t n, uint32_t k, uint32_t transpose,
                                               uint32_t out_dtype, std::vector<double>* est_us);
+
+// ---- tile_ir surface (t0mi_tile.cpp) ----
+// Byte offsets of the epilogue arguments in a TileGemm kernarg (0 = absent)
+// and the total size the lowered kernel declares.
+struct TileArgLayout {
+  uint32_t bias, scale, clamp_min, clamp_max, size;
+};
+TileArgLayout tile_arg_layout(const t0mi_tile_spec& s);
+// Checks a spec; fills the epilogue chain it encodes.
+bool tile_valid(const t0mi_tile_spec& s, EpiChain* chain, std::string* why);
+// The GemmConfig of the prebuilt gfx950 kernel that implements a spec
+// (same tile_m x tile_n x tile_k and layout), or false with the reason.
+bool tile_lower(const t0mi_tile_spec& s, t0mi_gemm_config* cfg, std::string* why);
+std::string tile_name(const t0mi_tile_spec& s);
+uint32_t tile_n_waves(const t0mi_tile_spec& s);
+uint32_t tile_wg_size(const t0mi_tile_spec& s);
+uint32_t tile_split_k(const t0mi_tile_spec& s);
 
 }  // namespace t0mi

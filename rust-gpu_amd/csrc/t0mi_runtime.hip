@@ -25,7 +25,8 @@ const GemmLaunchEntry* find_gemm_launch(const t0mi_gemm_config& c) {
   if (!wave_layout(c, &wm, &wn)) return nullptr;
   const bool nn = c.transpose == T0MI_NN;
   const GemmLaunchEntry* (*tables[])(size_t*) = {nn ? gemm_table_p0_nn : gemm_table_p0_nt,
-                                                nn ? gemm_table_p1_nn : gemm_table_p1_nt};
+                                                nn ? gemm_table_p1_nn : gemm_table_p1_nt,
+                                                nn ? gemm_table_p2_nn : gemm_table_p2_nt};
   for (auto tf : tables) {
     size_t n = 0;
     const GemmLaunchEntry* t = tf(&n);
@@ -85,11 +86,11 @@ int launch_gemm(t0mi_ctx* ctx, const t0mi_gemm_config& cfg, const GemmLaunchEntr
 
 // ------------------------------------------------------------ split-K reduce --
 // Deterministic reduction of split-K partial planes: y = sum_{p=0..sk-1} ws[p]
-// in ascending p, then bias / ReLU, then f32 or bf16 (RNE) store.
+// in ascending p, then the epilogue chain, then f32 or bf16 (RNE) store.
 __global__ __launch_bounds__(256) void t0mi_splitk_reduce(const float* __restrict__ ws, void* __restrict__ y,
                                                           const float* __restrict__ bias, uint32_t M, uint32_t N,
                                                           uint32_t ldy, uint32_t sk, uint32_t out_bf16,
-                                                          uint32_t epilogue) {
+                                                          EpiChain epi) {
   const size_t plane = (size_t)M * N;
   const size_t nvec = plane / 4;
   for (size_t v = blockIdx.x * (size_t)blockDim.x + threadIdx.x; v < nvec; v += (size_t)gridDim.x * blockDim.x) {
@@ -103,17 +104,13 @@ __global__ __launch_bounds__(256) void t0mi_splitk_reduce(const float* __restric
       s.z += t.z;
       s.w += t.w;
     }
-    if (epilogue != EPI_NONE) {
-      s.x += bias[n];
-      s.y += bias[n + 1];
-      s.z += bias[n + 2];
-      s.w += bias[n + 3];
-      if (epilogue == EPI_BIAS_RELU) {
-        s.x = fmaxf(s.x, 0.f);
-        s.y = fmaxf(s.y, 0.f);
-        s.z = fmaxf(s.z, 0.f);
-        s.w = fmaxf(s.w, 0.f);
-      }
+    if (epi.n) {
+      f32x4 bv = {0.f, 0.f, 0.f, 0.f};
+      if (bias) bv = f32x4{bias[n], bias[n + 1], bias[n + 2], bias[n + 3]};
+      s.x = epi_apply(s.x, bv.x, epi);
+      s.y = epi_apply(s.y, bv.y, epi);
+      s.z = epi_apply(s.z, bv.z, epi);
+      s.w = epi_apply(s.w, bv.w, epi);
     }
     if (out_bf16) {
       u32x2 o;
@@ -127,8 +124,27 @@ __global__ __launch_bounds__(256) void t0mi_splitk_reduce(const float* __restric
 }
 
 namespace t0mi {
+EpiChain chain_of(uint32_t gemm_gen_epilogue) {
+  EpiChain e;
+  memset(&e, 0, sizeof e);
+  if (gemm_gen_epilogue == T0MI_EPI_BIAS_ADD_STORE_F32) {
+    e.n = 1;
+    e.ops = EOP_BIAS;
+  } else if (gemm_gen_epilogue == T0MI_EPI_BIAS_ADD_RELU_STORE_F32) {
+    e.n = 2;
+    e.ops = EOP_BIAS | (EOP_RELU << 4);
+  }
+  return e;
+}
+
+static bool chain_uses(const EpiChain& e, uint32_t op) {
+  for (uint32_t i = 0; i < e.n; ++i)
+    if (((e.ops >> (4 * i)) & 0xFu) == op) return true;
+  return false;
+}
+
 int launch_splitk_reduce(t0mi_ctx* ctx, const float* ws, void* y, const float* bias, uint32_t M, uint32_t N,
-                         uint32_t ldy, uint32_t sk, uint32_t out_bf16, uint32_t epilogue) {
+                         uint32_t ldy, uint32_t sk, uint32_t out_bf16, const EpiChain& epilogue) {
   if (ctx->null_backend) return T0MI_OK;
   const size_t nvec = (size_t)M * N / 4;
   if (nvec == 0) return T0MI_OK;
@@ -386,6 +402,69 @@ static int wait_stream(t0mi_ctx* ctx) {
   return rc;
 }
 
+static float rd_f32(const uint8_t* p) {
+  const uint32_t u = rd_u32(p);
+  float f;
+  memcpy(&f, &u, 4);
+  return f;
+}
+
+// Dispatch of a lowered TileGemm with its own kernarg layout (tile_ir.rs:4570-4637
+// plus the epilogue arguments declared at :1014-1027).
+static int dispatch_tile(t0mi_ctx* ctx, const t0mi_kernel* k, const uint32_t grid[3], const uint8_t* ka) {
+  const t0mi_tile_spec& s = k->tile;
+  const uint64_t x = rd_u64(ka + 0), wt = rd_u64(ka + 8), y = rd_u64(ka + 16);
+  const uint32_t K = rd_u32(ka + 24), N = rd_u32(ka + 28), sks = rd_u32(ka + 32), yss = rd_u32(ka + 36);
+  uint32_t M = rd_u32(ka + 40);
+  const uint32_t sk = tile_split_k(s);
+  if (sks != (sk > 1 ? (uint32_t)__builtin_ctz(sk) : 0u))
+    return set_error(T0MI_ERR_INVALID, "split_k_shift %u does not match the spec's split_k %u", sks, sk);
+  if (!s.persistent) {
+    const uint32_t gx = grid[0] / k->wg_size, gy = grid[1] ? grid[1] : 1;
+    if (gy % sk) return set_error(T0MI_ERR_INVALID, "grid_y=%u not a multiple of split_k=%u", gy, sk);
+    const uint32_t tn = s.swap_grid ? gx : gy / sk, tm = s.swap_grid ? gy / sk : gx;
+    // build_kernargs leaves M = 0: fall back to the grid's (padded) row count.
+    if (M == 0) M = tm * s.tile_m;
+    if ((uint64_t)tn * s.tile_n < N || (uint64_t)tm * s.tile_m < M)
+      return set_error(T0MI_ERR_INVALID, "grid (%u x %u tiles) does not cover M=%u N=%u", tm, tn, M, N);
+  } else if (M == 0) {
+    return set_error(T0MI_ERR_INVALID, "persistent TileGemm dispatch needs M in the kernarg");
+  }
+  EpiChain chain = k->chain;
+  const uint64_t bias = k->lay.bias ? rd_u64(ka + k->lay.bias) : 0;
+  if (k->lay.scale) chain.scale = rd_f32(ka + k->lay.scale);
+  if (k->lay.clamp_min) {
+    chain.lo = rd_f32(ka + k->lay.clamp_min);
+    chain.hi = rd_f32(ka + k->lay.clamp_max);
+  }
+  if (sk == 1 || yss == 0)
+    // One output plane: split-K partitions are summed by the library.
+    return run_gemm(ctx, k->cfg, k->gemm, x, wt, y, bias, M, N, K, chain);
+  // Caller-provided partial planes (gemm_gen convention): partition p writes
+  // the raw f32 sum of its K range at Y + p * y_split_stride; no epilogue.
+  if (K % 8 || N % 8 || (K / sk) % 8)
+    return set_error(T0MI_ERR_INVALID, "K=%u and N=%u (and K/split_k) must be multiples of 8", K, N);
+  if ((uint64_t)yss < (uint64_t)M * N * 4u) return set_error(T0MI_ERR_INVALID, "y_split_stride smaller than a plane");
+  GemmParams p;
+  memset(&p, 0, sizeof p);
+  p.a = (const uint16_t*)x;
+  p.b = (const uint16_t*)wt;
+  p.y = (void*)y;
+  p.M = M;
+  p.N = N;
+  p.K = K;
+  p.lda = K;
+  p.ldb = s.transpose == T0MI_NN ? N : K;
+  p.ldy = N;
+  p.tiles_m = (M + k->cfg.tile_m - 1) / k->cfg.tile_m;
+  p.tiles_n = (N + k->cfg.tile_n - 1) / k->cfg.tile_n;
+  p.split_k = sk;
+  p.k_per_split = K / sk;
+  p.y_split_stride = yss;
+  p.xcd_remap = 1;
+  return launch_gemm(ctx, k->cfg, k->gemm, p);
+}
+
 static int dispatch_impl(t0mi_ctx* ctx, const t0mi_kernel* k, const uint32_t grid[3], const uint8_t* ka,
                          size_t ka_len) {
   int rc = check_ctx(ctx);
@@ -402,6 +481,7 @@ static int dispatch_impl(t0mi_ctx* ctx, const t0mi_kernel* k, const uint32_t gri
     memcpy(ctx->last_grid, grid, sizeof ctx->last_grid);
     ctx->last_ka.assign(ka, ka + ka_len);
   }
+  if (k->kind == KK_TILE) return dispatch_tile(ctx, k, grid, ka);
   const t0mi_gemm_config& c = k->cfg;
   const uint32_t sk = split_k_of(c);
   const uint32_t gx = grid[0] / k->wg_size, gy = grid[1] ? grid[1] : 1;
@@ -426,11 +506,11 @@ static int dispatch_impl(t0mi_ctx* ctx, const t0mi_kernel* k, const uint32_t gri
   p.split_k = sk;
   p.k_per_split = sk > 1 ? p.K / sk : p.K;  // K >> split_k_shift (gemm_gen.rs:769-775)
   p.out_bf16 = c.out_dtype == T0MI_OUT_BF16;
-  p.epilogue = c.epilogue;
+  p.epi = chain_of(c.epilogue);
   p.xcd_remap = 1;
   if (p.K % 8 || p.N % 8 || p.k_per_split % 8)
     return set_error(T0MI_ERR_INVALID, "K=%u and N=%u (and K/split_k) must be multiples of 8", p.K, p.N);
-  if (p.epilogue != EPI_NONE && !p.bias) return set_error(T0MI_ERR_INVALID, "bias epilogue with null bias");
+  if (p.epi.n && !p.bias) return set_error(T0MI_ERR_INVALID, "bias epilogue with null bias");
   if (sk > 1 && p.y_split_stride < (uint64_t)p.M * p.N * 4u)
     return set_error(T0MI_ERR_INVALID, "y_split_stride %llu smaller than an f32 plane", (unsigned long long)p.y_split_stride);
   return launch_gemm(ctx, c, k->gemm, p);
@@ -456,6 +536,66 @@ extern "C" int t0mi_wait_idle(t0mi_ctx* ctx) {
 
 // ---------------------------------------------------------- one-call GEMM ----
 
+namespace t0mi {
+int run_gemm(t0mi_ctx* ctx, const t0mi_gemm_config& cfg, const GemmLaunchEntry* e, uint64_t x, uint64_t b,
+             uint64_t y, uint64_t bias, uint32_t m, uint32_t n, uint32_t k, const EpiChain& epi) {
+  if (m == 0 || n == 0) return T0MI_OK;
+  if (k % 8) return set_error(T0MI_ERR_INVALID, "K=%u must be a multiple of 8", k);
+  if (n % 8) return set_error(T0MI_ERR_INVALID, "N=%u must be a multiple of 8", n);
+  if ((x | b | y) & 15) return set_error(T0MI_ERR_INVALID, "X, B and Y must be 16-byte aligned");
+  if (chain_uses(epi, EOP_BIAS) && !bias) return set_error(T0MI_ERR_INVALID, "bias epilogue with null bias");
+  if (bias & 3) return set_error(T0MI_ERR_INVALID, "bias must be 4-byte aligned");
+  const uint32_t sk = split_k_of(cfg);
+  GemmParams p;
+  memset(&p, 0, sizeof p);
+  p.a = (const uint16_t*)x;
+  p.b = (const uint16_t*)b;
+  p.bias = (const float*)bias;
+  p.M = m;
+  p.N = n;
+  p.K = k;
+  p.lda = k;
+  p.ldb = cfg.transpose == T0MI_NN ? n : k;
+  p.ldy = n;
+  p.tiles_m = (m + cfg.tile_m - 1) / cfg.tile_m;
+  p.tiles_n = (n + cfg.tile_n - 1) / cfg.tile_n;
+  p.split_k = sk;
+  p.epi = epi;
+  p.out_bf16 = cfg.out_dtype == T0MI_OUT_BF16;
+  p.xcd_remap = 1;
+  int rc;
+  if (k == 0) {
+    // Empty contraction: the sum is zero (plus epilogue).
+    if (ctx->null_backend) return T0MI_OK;
+    rc = ensure_workspace(ctx, (size_t)m * n * 4);
+    if (rc) return rc;
+    hipError_t he = hipMemsetAsync(ctx->ws, 0, (size_t)m * n * 4, ctx->stream);
+    if (he != hipSuccess) return hip_fail(he, "hipMemsetAsync");
+    return launch_splitk_reduce(ctx, (const float*)ctx->ws, (void*)y, (const float*)bias, m, n, n, 1u, p.out_bf16,
+                                epi);
+  }
+  if (sk == 1) {
+    p.k_per_split = k;
+    p.y = (void*)y;
+    return launch_gemm(ctx, cfg, e, p);
+  }
+  // Split-K: partitions of whole K tiles write f32 planes into the workspace,
+  // then a reduce pass sums them in partition order.
+  const uint32_t kt = (k + cfg.tile_k - 1) / cfg.tile_k;
+  p.k_per_split = ((kt + sk - 1) / sk) * cfg.tile_k;
+  const size_t plane = (size_t)m * n * 4;
+  rc = ensure_workspace(ctx, plane * sk);
+  if (rc) return rc;
+  p.y = ctx->ws;
+  p.ldy = n;
+  p.y_split_stride = plane;
+  rc = launch_gemm(ctx, cfg, e, p);
+  if (rc || ctx->null_backend) return rc;
+  return launch_splitk_reduce(ctx, (const float*)ctx->ws, (void*)y, (const float*)bias, m, n, n, sk, p.out_bf16,
+                              epi);
+}
+}  // namespace t0mi
+
 extern "C" int t0mi_gemm(t0mi_ctx* ctx, const t0mi_gemm_config* cfg, uint64_t x, uint64_t b, uint64_t y,
                          uint64_t bias, uint32_t m, uint32_t n, uint32_t k) {
   int rc = check_ctx(ctx);
@@ -467,56 +607,62 @@ extern "C" int t0mi_gemm(t0mi_ctx* ctx, const t0mi_gemm_config* cfg, uint64_t x,
                      why.c_str());
   const GemmLaunchEntry* e = find_gemm_launch(*cfg);
   if (!e) return set_error(T0MI_ERR_NO_KERNEL, "[t0mi] no prebuilt gfx950 kernel for '%s'", config_name(*cfg).c_str());
-  if (m == 0 || n == 0) return T0MI_OK;
-  if (k % 8) return set_error(T0MI_ERR_INVALID, "K=%u must be a multiple of 8", k);
-  if (n % 8) return set_error(T0MI_ERR_INVALID, "N=%u must be a multiple of 8", n);
-  if ((x | b | y) & 15) return set_error(T0MI_ERR_INVALID, "X, B and Y must be 16-byte aligned");
-  if (cfg->epilogue != T0MI_EPI_STORE_F32 && !bias) return set_error(T0MI_ERR_INVALID, "bias epilogue with null bias");
-  const uint32_t sk = split_k_of(*cfg);
-  GemmParams p;
-  memset(&p, 0, sizeof p);
-  p.a = (const uint16_t*)x;
-  p.b = (const uint16_t*)b;
-  p.bias = (const float*)bias;
-  p.M = m;
-  p.N = n;
-  p.K = k;
-  p.lda = k;
-  p.ldb = cfg->transpose == T0MI_NN ? n : k;
-  p.ldy = n;
-  p.tiles_m = (m + cfg->tile_m - 1) / cfg->tile_m;
-  p.tiles_n = (n + cfg->tile_n - 1) / cfg->tile_n;
-  p.split_k = sk;
-  p.epilogue = cfg->epilogue;
-  p.out_bf16 = cfg->out_dtype == T0MI_OUT_BF16;
-  p.xcd_remap = 1;
-  if (k == 0) {
-    // Empty contraction: the sum is zero (plus epilogue).
-    if (ctx->null_backend) return T0MI_OK;
-    rc = ensure_workspace(ctx, (size_t)m * n * 4);
-    if (rc) return rc;
-    hipError_t he = hipMemsetAsync(ctx->ws, 0, (size_t)m * n * 4, ctx->stream);
-    if (he != hipSuccess) return hip_fail(he, "hipMemsetAsync");
-    return launch_splitk_reduce(ctx, (const float*)ctx->ws, (void*)y, (const float*)bias, m, n, n, 1u, p.out_bf16,
-                                p.epilogue);
+  return run_gemm(ctx, *cfg, e, x, b, y, bias, m, n, k, chain_of(cfg->epilogue));
+}
+
+// ------------------------------------------------------------ tile_ir GEMM ----
+
+extern "C" int t0mi_tile_kernel_get(t0mi_ctx* ctx, const t0mi_tile_spec* s, t0mi_kernel** out) {
+  if (!ctx || !s || !out) return set_error(T0MI_ERR_INVALID, "null argument");
+  EpiChain chain;
+  std::string why;
+  if (!tile_valid(*s, &chain, &why))
+    return set_error(T0MI_ERR_INVALID, "[t0mi] TileGemm '%s' invalid: %s", tile_name(*s).c_str(), why.c_str());
+  t0mi_gemm_config cfg;
+  if (!tile_lower(*s, &cfg, &why))
+    return set_error(T0MI_ERR_NO_KERNEL, "[t0mi] TileGemm '%s': %s", tile_name(*s).c_str(), why.c_str());
+  const GemmLaunchEntry* e = find_gemm_launch(cfg);
+  if (!e) return set_error(T0MI_ERR_NO_KERNEL, "[t0mi] no prebuilt gfx950 kernel for '%s'", tile_name(*s).c_str());
+  const std::string name = tile_name(*s);
+  std::lock_guard<std::mutex> lk(ctx->mu);
+  auto it = ctx->kernels.find(name);
+  if (it != ctx->kernels.end()) {
+    *out = it->second.get();
+    return T0MI_OK;
   }
-  if (sk == 1) {
-    p.k_per_split = k;
-    p.y = (void*)y;
-    return launch_gemm(ctx, *cfg, e, p);
-  }
-  // Split-K: partitions of whole K tiles write f32 planes into the workspace,
-  // then a reduce pass sums them in partition order.
-  const uint32_t kt = (k + cfg->tile_k - 1) / cfg->tile_k;
-  p.k_per_split = ((kt + sk - 1) / sk) * cfg->tile_k;
-  const size_t plane = (size_t)m * n * 4;
-  rc = ensure_workspace(ctx, plane * sk);
+  std::unique_ptr<t0mi_kernel> k(new t0mi_kernel());
+  k->kind = KK_TILE;
+  k->cfg = cfg;
+  k->tile = *s;
+  k->lay = tile_arg_layout(*s);
+  k->chain = chain;
+  k->name = name;
+  k->kernarg_size = k->lay.size;
+  k->lds_size = t0mi_tile_lds_total(s);
+  k->wg_size = tile_wg_size(*s);
+  k->gemm = e;
+  *out = k.get();
+  ctx->kernels[name] = std::move(k);
+  return T0MI_OK;
+}
+
+extern "C" int t0mi_tile_gemm(t0mi_ctx* ctx, const t0mi_tile_spec* s, uint64_t x, uint64_t wt, uint64_t y,
+                              uint32_t m, uint32_t n, uint32_t k, uint64_t bias, float scale, float clamp_min,
+                              float clamp_max) {
+  int rc = check_ctx(ctx);
   if (rc) return rc;
-  p.y = ctx->ws;
-  p.ldy = n;
-  p.y_split_stride = plane;
-  rc = launch_gemm(ctx, *cfg, e, p);
-  if (rc || ctx->null_backend) return rc;
-  return launch_splitk_reduce(ctx, (const float*)ctx->ws, (void*)y, (const float*)bias, m, n, n, sk, p.out_bf16,
-                              p.epilogue);
+  if (!s) return set_error(T0MI_ERR_INVALID, "null spec");
+  EpiChain chain;
+  std::string why;
+  if (!tile_valid(*s, &chain, &why))
+    return set_error(T0MI_ERR_INVALID, "[t0mi] TileGemm '%s' invalid: %s", tile_name(*s).c_str(), why.c_str());
+  t0mi_gemm_config cfg;
+  if (!tile_lower(*s, &cfg, &why))
+    return set_error(T0MI_ERR_NO_KERNEL, "[t0mi] TileGemm '%s': %s", tile_name(*s).c_str(), why.c_str());
+  const GemmLaunchEntry* e = find_gemm_launch(cfg);
+  if (!e) return set_error(T0MI_ERR_NO_KERNEL, "[t0mi] no prebuilt gfx950 kernel for '%s'", tile_name(*s).c_str());
+  chain.scale = scale;
+  chain.lo = clamp_min;
+  chain.hi = clamp_max;
+  return run_gemm(ctx, cfg, e, x, wt, y, bias, m, n, k, chain);
 }

@@ -412,7 +412,7 @@ extern "C" int t0mi_w4a16_gemm(t0mi_ctx* ctx, uint64_t a, uint64_t qweight, uint
     if (e != hipSuccess) return hip_fail(e, "w4a16 launch");
     if (ky > 1) {
       rc = launch_splitk_reduce(ctx, (const float*)ctx->ws, (char*)y + (size_t)r0 * n * ob, nullptr, mr, n, n, ky,
-                                p.out_bf16, 0u);
+                                p.out_bf16, EpiChain{});
       if (rc) return rc;
     }
   }

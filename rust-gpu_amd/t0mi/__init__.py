@@ -67,6 +67,66 @@ class GemmConfig(ctypes.Structure):
         return f"GemmConfig({self.name()})"
 
 
+# tile_ir EpilogueOp (src/t0/tile_ir.rs:40-58)
+BIAS_ADD, SCALE, RELU, SILU, GELU, ABS, NEG, CLAMP = range(8)
+EPILOGUE_NAMES = ("bias", "scale", "relu", "silu", "gelu", "abs", "neg", "clamp")
+
+
+class TileGemm(ctypes.Structure):
+    """Mirror of ``TileGemm`` (src/t0/tile_ir.rs:100-152) plus out_dtype."""
+    _fields_ = ([(n, ctypes.c_uint32) for n in (
+        "tile_m", "tile_n", "tile_k", "wgp_mode", "double_buffer", "triple_buffer", "split_k", "swap_grid",
+        "transpose", "acc_swap", "n_epilogue")] + [("epilogue", ctypes.c_uint32 * 8)] +
+        [(n, ctypes.c_uint32) for n in ("persistent", "waves_per_wg", "wmma_format", "out_dtype")])
+
+    def copy(self, **kw) -> "TileGemm":
+        c = TileGemm()
+        ctypes.memmove(ctypes.byref(c), ctypes.byref(self), ctypes.sizeof(TileGemm))
+        for k, v in kw.items():
+            if k == "epilogue":
+                c.set_epilogue(v)
+            else:
+                setattr(c, k, v)
+        return c
+
+    def set_epilogue(self, ops) -> "TileGemm":
+        """``with_epilogue`` (tile_ir.rs:709-712)."""
+        ops = list(ops)
+        if len(ops) > 8:
+            raise ValueError("at most 8 epilogue ops")
+        self.n_epilogue = len(ops)
+        for i in range(8):
+            self.epilogue[i] = ops[i] if i < len(ops) else 0
+        return self
+
+    def add_epilogue(self, op: int) -> "TileGemm":
+        """``add_epilogue`` (tile_ir.rs:704-707)."""
+        return self.set_epilogue(self.epilogue_ops() + [op])
+
+    def epilogue_ops(self) -> list:
+        return [self.epilogue[i] for i in range(self.n_epilogue)]
+
+    def name(self) -> str:
+        buf = ctypes.create_string_buffer(256)
+        lib().t0mi_tile_name(ctypes.byref(self), buf, 256)
+        return buf.value.decode()
+
+    def n_waves(self) -> int:
+        return lib().t0mi_tile_n_waves(ctypes.byref(self))
+
+    def wg_size(self) -> int:
+        return lib().t0mi_tile_wg_size(ctypes.byref(self))
+
+    def lds_total(self) -> int:
+        return lib().t0mi_tile_lds_total(ctypes.byref(self))
+
+    def kernarg_size(self) -> int:
+        return lib().t0mi_tile_kernarg_size(ctypes.byref(self))
+
+    def __repr__(self):
+        return f"TileGemm({self.name()})"
+
+
 _lib = None
 
 # Every symbol declared in include/t0mi.h, with (restype, argtypes).
@@ -77,6 +137,8 @@ _SZ = ctypes.c_size_t
 _I = ctypes.c_int
 _CFG = ctypes.POINTER(GemmConfig)
 _CHARP = ctypes.c_char_p
+_F32 = ctypes.c_float
+_TS = ctypes.POINTER(TileGemm)
 SIGNATURES = {
     "t0mi_last_error": (_CHARP, []),
     "t0mi_abi_version": (_I, []),
@@ -132,6 +194,22 @@ SIGNATURES = {
     "t0mi_tuner_cache_path": (_I, [_P, _U32, _U32, _U32, _U32, _U32, _CHARP, _SZ]),
     "t0mi_tuner_report": (_I, [_P, _CHARP, _SZ]),
     "t0mi_auto_gemm": (_I, [_P, _U64, _U64, _U64, _U32, _U32, _U32, ctypes.POINTER(ctypes.c_double)]),
+    "t0mi_tile_preset": (_I, [_CHARP, _TS]),
+    "t0mi_tile_preset_names": (_CHARP, []),
+    "t0mi_tile_name": (_I, [_TS, _CHARP, _SZ]),
+    "t0mi_tile_n_waves": (_U32, [_TS]),
+    "t0mi_tile_wg_size": (_U32, [_TS]),
+    "t0mi_tile_lds_total": (_U32, [_TS]),
+    "t0mi_tile_auto_select": (_I, [_U32, _U32, _U32, _U32, _TS]),
+    "t0mi_tile_kernarg_size": (_U32, [_TS]),
+    "t0mi_tile_build_kernargs": (_I, [_U64, _U64, _U64, _U32, _U32, _TS, _P, _SZ]),
+    "t0mi_tile_build_kernargs_m": (_I, [_U64, _U64, _U64, _U32, _U32, _U32, _TS, _P, _SZ]),
+    "t0mi_tile_build_kernargs_m_with_counter": (_I, [_U64, _U64, _U64, _U32, _U32, _U32, _TS, _U64, _U32, _U32,
+                                                     _P, _SZ]),
+    "t0mi_tile_append_epilogue_args": (_I, [_TS, _U64, _F32, _F32, _F32, _P, _SZ, ctypes.POINTER(_SZ)]),
+    "t0mi_tile_compute_grid": (_I, [_TS, _U32, _U32, ctypes.POINTER(_U32)]),
+    "t0mi_tile_kernel_get": (_I, [_P, _TS, ctypes.POINTER(_P)]),
+    "t0mi_tile_gemm": (_I, [_P, _TS, _U64, _U64, _U64, _U32, _U32, _U32, _U64, _F32, _F32, _F32]),
     "t0mi_w4a16_gemm": (_I, [_P, _U64, _U64, _U64, _U64, _U32, _U64, _U32, _U32, _U32, _U32, _U32]),
     "t0mi_dequant_int4": (_I, [_P, _U64, _U64, _U64, _U32, _U64, _U32, _U32, _U32, _U32]),
 }
@@ -143,6 +221,14 @@ def lib():
         if not os.path.exists(LIB_PATH):
             raise ImportError(f"libt0mi.so not built at {LIB_PATH}; run __graft_entry__.build() "
                               f"(make -C {_PKG_ROOT})")
+        # One HIP runtime per process: when torch is installed, load it first so
+        # libt0mi binds to the HIP runtime torch already mapped (same soname).
+        # Loaded the other way round, the two runtimes contend for the device
+        # and the second to initialise sees no GPU.
+        try:
+            import torch  # noqa: F401
+        except ImportError:
+            pass
         L = ctypes.CDLL(LIB_PATH)
         for name, (res, args) in SIGNATURES.items():
             f = getattr(L, name)
@@ -258,6 +344,68 @@ def cached_auto_select(m: int, k: int, n: int) -> GemmConfig:
     return c
 
 
+# ------------------------------------------------------------ tile_ir ----
+
+def tile_preset(name: str) -> TileGemm:
+    """``TileGemm::<name>()`` (src/t0/tile_ir.rs:156-604)."""
+    s = TileGemm()
+    check(lib().t0mi_tile_preset(name.encode(), ctypes.byref(s)))
+    return s
+
+
+def tile_preset_names() -> list:
+    return lib().t0mi_tile_preset_names().decode().split(",")
+
+
+def tile_auto_select(m: int, k: int, n: int, transpose: int = NT) -> TileGemm:
+    """``tile_auto_select(m, k, n, transpose)`` (src/t0/tile_ir.rs:740-870)."""
+    s = TileGemm()
+    check(lib().t0mi_tile_auto_select(m, k, n, transpose, ctypes.byref(s)))
+    return s
+
+
+def _ka(fn, *args) -> bytes:
+    buf = (ctypes.c_uint8 * 128)()
+    n = fn(*args, buf, 128)
+    if n < 0:
+        check(n)
+    return bytes(buf[:n])
+
+
+def tile_build_kernargs(x: int, wt: int, y: int, k: int, n: int, spec: TileGemm) -> bytes:
+    """``build_kernargs`` (tile_ir.rs:4570-4593): 44 bytes, M slot 0."""
+    return _ka(lib().t0mi_tile_build_kernargs, x, wt, y, k, n, ctypes.byref(spec))
+
+
+def tile_build_kernargs_m(x: int, wt: int, y: int, k: int, n: int, m: int, spec: TileGemm) -> bytes:
+    """``build_kernargs_m`` (tile_ir.rs:4595-4602)."""
+    return _ka(lib().t0mi_tile_build_kernargs_m, x, wt, y, k, n, m, ctypes.byref(spec))
+
+
+def tile_build_kernargs_m_with_counter(x: int, wt: int, y: int, k: int, n: int, m: int, spec: TileGemm,
+                                       counter: int, n_tiles_n_shift: int, tiles_per_wg: int) -> bytes:
+    """``build_kernargs_m_with_counter`` (tile_ir.rs:4604-4637)."""
+    return _ka(lib().t0mi_tile_build_kernargs_m_with_counter, x, wt, y, k, n, m, ctypes.byref(spec), counter,
+               n_tiles_n_shift, tiles_per_wg)
+
+
+def tile_append_epilogue_args(spec: TileGemm, ka: bytes, bias: int = 0, scale: float = 1.0,
+                              clamp_min: float = 0.0, clamp_max: float = 0.0) -> bytes:
+    """The epilogue kernargs lower_gemm declares (tile_ir.rs:1014-1027), after the GEMM ones."""
+    buf = (ctypes.c_uint8 * 128).from_buffer_copy(ka + b"\0" * (128 - len(ka)))
+    n = ctypes.c_size_t(len(ka))
+    check(lib().t0mi_tile_append_epilogue_args(ctypes.byref(spec), bias, scale, clamp_min, clamp_max, buf, 128,
+                                               ctypes.byref(n)))
+    return bytes(buf[: n.value])
+
+
+def tile_compute_grid(spec: TileGemm, m: int, n: int):
+    """``compute_grid`` (tile_ir.rs:4645-4666), in work-items."""
+    g = (ctypes.c_uint32 * 3)()
+    check(lib().t0mi_tile_compute_grid(ctypes.byref(spec), m, n, g))
+    return (g[0], g[1], g[2])
+
+
 # ------------------------------------------------------------ runtime ----
 
 class Kernel:
@@ -355,6 +503,17 @@ class Runtime:
         h = ctypes.c_void_p()
         check(lib().t0mi_kernel_get(self.handle, ctypes.byref(cfg), ctypes.byref(h)))
         return Kernel(h, self)
+
+    def tile_kernel(self, spec: TileGemm) -> Kernel:
+        """``lower_gemm(&spec)`` + compile + load -> the prebuilt gfx950 kernel for the spec."""
+        h = ctypes.c_void_p()
+        check(lib().t0mi_tile_kernel_get(self.handle, ctypes.byref(spec), ctypes.byref(h)))
+        return Kernel(h, self)
+
+    def tile_gemm(self, spec: TileGemm, x: int, wt: int, y: int, m: int, n: int, k: int, bias: int = 0,
+                  scale: float = 1.0, clamp_min: float = 0.0, clamp_max: float = 0.0) -> None:
+        check(lib().t0mi_tile_gemm(self.handle, ctypes.byref(spec), x, wt, y, m, n, k, bias, scale, clamp_min,
+                                   clamp_max))
 
     def dispatch(self, k: Kernel, grid: Sequence[int], ka: bytes, sync: bool = True) -> int:
         g = (ctypes.c_uint32 * 3)(*(list(grid) + [1] * (3 - len(grid))))

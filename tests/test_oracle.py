@@ -240,3 +240,38 @@ def test_w4a16_oracle_is_dequant_then_gemm():
     for kk in range(K):
         ref = (ref + (af[:, kk:kk + 1] * wf[kk:kk + 1, :]).astype(np.float32)).astype(np.float32)
     assert np.array_equal(y, ref)
+
+
+# ------------------------------------------------------- epilogue chain ----
+
+def test_epilogue_closed_forms():
+    """Each EpilogueOp (src/t0/tile_ir.rs:3400-3540) against values fixed by its definition."""
+    y = np.array([[-3.0, -0.5, 0.0, 0.5, 3.0, 40.0, -40.0, 1.0]], dtype=np.float32)
+    bias = np.arange(8, dtype=np.float32)
+    assert np.array_equal(oracle.epilogue(y, [0], bias=bias), y + bias)
+    assert np.array_equal(oracle.epilogue(y, [1], scale=0.25), y * np.float32(0.25))
+    assert np.array_equal(oracle.epilogue(y, [2]), np.maximum(y, 0))
+    assert np.array_equal(oracle.epilogue(y, [5]), np.abs(y))
+    assert np.array_equal(oracle.epilogue(y, [6]), -y)
+    assert np.array_equal(oracle.epilogue(y, [7], clamp_min=-1.0, clamp_max=2.0), np.clip(y, -1.0, 2.0))
+    silu = oracle.epilogue(y, [3])[0]
+    assert silu[2] == 0.0
+    assert abs(silu[5] - 40.0) < 1e-5 and abs(silu[6]) < 1e-15      # tails: x and 0
+    assert abs(silu[7] - 1.0 / (1.0 + np.exp(-1.0))) < 1e-7           # silu(1) = sigmoid(1)
+    assert abs(silu[0] - (-3.0 / (1.0 + np.exp(3.0)))) < 1e-6
+    gelu = oracle.epilogue(y, [4])[0]
+    assert gelu[2] == 0.0
+    assert abs(gelu[7] - 1.0 / (1.0 + np.exp(-1.702))) < 1e-7          # sigmoid form at 1
+    assert abs(gelu[4] - 3.0 / (1.0 + np.exp(-1.702 * 3.0))) < 1e-6
+
+
+def test_epilogue_order_of_application():
+    """Ops apply in list order: bias then relu differs from relu then bias."""
+    y = np.array([[-2.0, 1.0]], dtype=np.float32)
+    b = np.array([1.0, -3.0], dtype=np.float32)
+    assert np.array_equal(oracle.epilogue(y, [0, 2], bias=b), [[0.0, 0.0]])
+    assert np.array_equal(oracle.epilogue(y, [2, 0], bias=b), [[1.0, -2.0]])
+    assert np.array_equal(oracle.epilogue(y, [6, 7], clamp_min=-1.5, clamp_max=1.5), [[1.5, -1.0]])
+    assert np.array_equal(oracle.epilogue(y, []), y)
+    with pytest.raises(ValueError):
+        oracle.epilogue(y, [0])
