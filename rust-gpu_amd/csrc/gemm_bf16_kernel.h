@@ -84,6 +84,13 @@ __device__ __forceinline__ uint16_t f32_to_bf16_rne(float f) {
   return __builtin_bit_cast(uint16_t, h);
 }
 
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+typedef float f32x2_t __attribute__((ext_vector_type(2)));
+// Two floats -> packed bf16 pair (lo in bits 0..15), RNE: one v_cvt_pk_bf16_f32.
+__device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2_t{lo, hi}, bf16x2_t));
+}
+
 // XOR swizzle of 16-byte chunks inside a K-contiguous LDS row of KC chunks.
 // Any 8 consecutive rows (aligned to 8) reading the same logical chunk land in
 // 8 distinct 16-byte slots of a 128-byte bank line.
@@ -104,21 +111,26 @@ __device__ __forceinline__ int swz_nn(int k) { return (k & 3) << 1; }
 // ids that run on the same XCD (same L2) are made contiguous, then tiles are
 // walked in groups of GROUP_M tile rows so each XCD works on a compact block
 // of output tiles (shared A rows / B columns stay L2-resident).
-__device__ __forceinline__ void tile_coords(const GemmParams& p, int& tm, int& tn, int& part) {
+__device__ __forceinline__ void tile_coords_of(uint32_t tiles_m, uint32_t tiles_n, uint32_t xcd_remap, int& tm,
+                                               int& tn, int& part) {
   uint32_t nwg = gridDim.x * gridDim.y;
   uint32_t lin = blockIdx.x + blockIdx.y * gridDim.x;
-  if (p.xcd_remap && (nwg % 8u) == 0u) lin = (lin % 8u) * (nwg / 8u) + lin / 8u;
-  uint32_t tiles = p.tiles_m * p.tiles_n;
+  if (xcd_remap && (nwg % 8u) == 0u) lin = (lin % 8u) * (nwg / 8u) + lin / 8u;
+  uint32_t tiles = tiles_m * tiles_n;
   part = (int)(lin / tiles);
   uint32_t t = lin % tiles;
   const uint32_t GROUP_M = 4;
-  uint32_t group_size = GROUP_M * p.tiles_n;
+  uint32_t group_size = GROUP_M * tiles_n;
   uint32_t g = t / group_size;
   uint32_t first_m = g * GROUP_M;
-  uint32_t gm = p.tiles_m - first_m < GROUP_M ? p.tiles_m - first_m : GROUP_M;
+  uint32_t gm = tiles_m - first_m < GROUP_M ? tiles_m - first_m : GROUP_M;
   uint32_t r = t % group_size;
   tm = (int)(first_m + r % gm);
   tn = (int)(r / gm);
+}
+
+__device__ __forceinline__ void tile_coords(const GemmParams& p, int& tm, int& tn, int& part) {
+  tile_coords_of(p.tiles_m, p.tiles_n, p.xcd_remap, tm, tn, part);
 }
 
 // 16-byte global -> LDS DMA: lane i's 16 bytes land at LDS byte address

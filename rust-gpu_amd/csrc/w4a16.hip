@@ -21,6 +21,7 @@
 #include <string.h>
 
 #include "t0mi_ctx.h"
+#include "w4a16_prefill.h"
 
 using namespace t0mi;
 
@@ -343,6 +344,10 @@ static int hip_fail(hipError_t e, const char* what) {
   return set_error(T0MI_ERR_HIP, "%s: %s", what, hipGetErrorString(e));
 }
 
+// Up to this many rows the decode kernel (16-row slabs) runs; above it the
+// MFMA prefill kernel.
+static constexpr uint32_t kDecodeMaxRows = 32;
+
 extern "C" int t0mi_w4a16_gemm(t0mi_ctx* ctx, uint64_t a, uint64_t qweight, uint64_t scales, uint64_t qzeros,
                                uint32_t zp_const, uint64_t y, uint32_t m, uint32_t k, uint32_t n, uint32_t group,
                                uint32_t out_dtype) {
@@ -369,6 +374,42 @@ extern "C" int t0mi_w4a16_gemm(t0mi_ctx* ctx, uint64_t a, uint64_t qweight, uint
   p.group = group;
   p.zp_const = zp_const;
   p.out_bf16 = out_dtype == T0MI_OUT_BF16;
+  if (m > kDecodeMaxRows && (group & (group - 1)) == 0) {
+    // Many rows: dequant fused into the MFMA K-loop, weights read once per tile column.
+    W4PrefillParams q;
+    memset(&q, 0, sizeof q);
+    q.a = (const uint16_t*)a;
+    q.w = (const uint32_t*)qweight;
+    q.scales = (const uint16_t*)scales;
+    q.zeros = (const uint32_t*)qzeros;
+    q.y = (void*)y;
+    q.M = m;
+    q.N = n;
+    q.K = k;
+    q.group_shift = (uint32_t)__builtin_ctz(group);
+    q.zp_const = zp_const;
+    q.out_bf16 = p.out_bf16;
+    q.xcd_remap = 1;
+    const bool big = m >= 1024;
+    const uint32_t bm = big ? 256 : 128, bn = big ? 256 : 128;
+    q.tiles_m = (m + bm - 1) / bm;
+    q.tiles_n = (n + bn - 1) / bn;
+    const dim3 grid(q.tiles_n, q.tiles_m);
+    const bool z = qzeros != 0;
+    if (big) {
+      if (z)
+        hipLaunchKernelGGL((w4a16_prefill_kernel<256, 256, 64, 2, 4, true>), grid, dim3(512), 0, ctx->stream, q);
+      else
+        hipLaunchKernelGGL((w4a16_prefill_kernel<256, 256, 64, 2, 4, false>), grid, dim3(512), 0, ctx->stream, q);
+    } else {
+      if (z)
+        hipLaunchKernelGGL((w4a16_prefill_kernel<128, 128, 64, 2, 2, true>), grid, dim3(256), 0, ctx->stream, q);
+      else
+        hipLaunchKernelGGL((w4a16_prefill_kernel<128, 128, 64, 2, 2, false>), grid, dim3(256), 0, ctx->stream, q);
+    }
+    hipError_t e = hipGetLastError();
+    return e == hipSuccess ? T0MI_OK : hip_fail(e, "w4a16 prefill launch");
+  }
   constexpr int WAVES = 8, KBW = 16;
   const uint32_t kb_tot = k / 32;
   const uint32_t ky = (kb_tot + WAVES * KBW - 1) / (WAVES * KBW);

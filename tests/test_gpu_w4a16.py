@@ -57,7 +57,7 @@ def check(y, ref, a, wf, k, rel_max):
     (5, 256, 136, 32, True),
     (16, 1024, 520, 64, True),
     (16, 8192, 256, 128, False),     # K beyond one workgroup's range -> split + reduce
-    (37, 384, 200, 128, True),       # M > 16 -> several row slabs
+    (32, 384, 200, 128, True),       # M > 16 -> several row slabs
     (3, 4096, 64, 4096, False),      # group larger than a wave's K range
 ])
 def test_w4a16_vs_oracle(rt, m, k, n, group, pgz):
@@ -68,6 +68,45 @@ def test_w4a16_vs_oracle(rt, m, k, n, group, pgz):
     check(y32, ref, a, wf, k, 1e-5)
     yb = run_w4a16(rt, a, w, s, z, m, k, n, group, out_bf16=True)
     check(yb, ref, a, wf, k, 5e-3)
+
+
+@pytest.mark.parametrize("m,k,n,group,pgz", [
+    (37, 384, 200, 128, True),       # just above the decode range: 128x128 tiles
+    (64, 256, 136, 32, True),
+    (300, 512, 264, 64, False),      # ragged M and N tiles
+    (1024, 1024, 512, 128, True),    # 256x256 tiles
+    (1100, 384, 520, 128, False),
+])
+def test_w4a16_prefill_vs_oracle(rt, m, k, n, group, pgz):
+    """Prefill rows: the dequantised weight is rounded to bf16 (RNE) inside the K-loop.
+    Against the oracle GEMM on RNE(exact dequant) weights the result matches to fp32
+    accumulation noise (this pins the in-loop dequant bit for bit up to summation order);
+    against the exact-dequant oracle it is within the GEMM tolerance."""
+    a, q, w, s, z = make_case(m, k, n, group, pgz, seed=0x60)
+    wf = oracle.dequant_qweight_f32(w, s, z, group, 8)
+    ref_exact = oracle.w4a16_gemm(a, w, s, z, group, 8)
+    ref_rne = oracle.gemm_bf16(a, oracle.bf16_rne(wf), "nn")
+    y32 = run_w4a16(rt, a, w, s, z, m, k, n, group, out_bf16=False)
+    check(y32, ref_rne, a, wf, k, 1e-5)
+    check(y32, ref_exact, a, wf, k, 5e-3)
+    yb = run_w4a16(rt, a, w, s, z, m, k, n, group, out_bf16=True)
+    check(yb, ref_exact, a, wf, k, 6e-3)
+
+
+def test_w4a16_prefill_config5_sampled_rows(rt):
+    """BASELINE config 5 at full size (A[4096,4096] x int4 W[4096,14336], g128, per-group
+    zeros, bf16 out); 48 rows spread over M checked against the oracle."""
+    m, k, n, group = 4096, 4096, 14336, 128
+    a = oracle.normal_bf16((m, k), oracle.seeds(4)[0], 0.0, 1.0)
+    w = oracle.pack_qweight(oracle.nibbles((k, n), oracle.seeds(4)[1]))
+    s = oracle.uniform_bf16((k // group, n), oracle.seeds(4)[2], 0.005, 0.02)
+    z = oracle.pack_qzeros(oracle.nibbles((k // group, n), oracle.seeds(4)[3]))
+    y = run_w4a16(rt, a, w, s, z, m, k, n, group, out_bf16=True)
+    rows = np.unique(np.concatenate([np.arange(0, m, 97), [m - 1]]))[:48]
+    wf = oracle.dequant_qweight_f32(w, s, z, group, 8)
+    ref = oracle.w4a16_gemm(np.ascontiguousarray(a[rows]), w, s, z, group, 8)
+    check(y[rows], ref, a[rows], wf, k, 6e-3)
+    assert np.isfinite(y).all()
 
 
 def test_w4a16_deterministic(rt):
