@@ -33,6 +33,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <utility>
+
 #include "epi_chain.h"
 
 namespace t0mi {
@@ -91,6 +93,48 @@ __device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
   return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2_t{lo, hi}, bf16x2_t));
 }
 
+// Calls f(std::integral_constant<int, 0>) .. f(std::integral_constant<int, N-1>):
+// a loop the compiler cannot leave rolled, for register arrays that must only
+// be indexed by constants.
+template <typename F, int... I>
+__device__ __forceinline__ void static_for_impl(F& f, std::integer_sequence<int, I...>) {
+  (f(std::integral_constant<int, I>{}), ...);
+}
+template <int N, typename F>
+__device__ __forceinline__ void static_for(F&& f) {
+  static_for_impl(f, std::make_integer_sequence<int, N>{});
+}
+
+// Stores one 32x32 accumulator block.  Lane l holds rows m (one per lane) and
+// columns n + 8*g + {0..3}, g = 0..3 (n already includes 4*(l >> 5)).  Columns
+// at or beyond N are skipped (the tile's N tail).
+__device__ __forceinline__ void store_block(const GemmParams& p, const f32x16& a, char* ybase, int m, int n,
+                                            bool partial_plane) {
+#pragma unroll
+  for (int g = 0; g < 4; ++g) {
+    const int nc = n + g * 8;
+    if (nc >= (int)p.N) continue;
+    float v0 = a[g * 4 + 0], v1 = a[g * 4 + 1], v2 = a[g * 4 + 2], v3 = a[g * 4 + 3];
+    if (!partial_plane && p.epi.n) {
+      f32x4 bv = {0.0f, 0.0f, 0.0f, 0.0f};
+      if (p.bias) bv = f32x4{p.bias[nc], p.bias[nc + 1], p.bias[nc + 2], p.bias[nc + 3]};
+      v0 = epi_apply(v0, bv.x, p.epi);
+      v1 = epi_apply(v1, bv.y, p.epi);
+      v2 = epi_apply(v2, bv.z, p.epi);
+      v3 = epi_apply(v3, bv.w, p.epi);
+    }
+    if (!partial_plane && p.out_bf16) {
+      u32x2 o;
+      o.x = pack_bf16x2(v0, v1);
+      o.y = pack_bf16x2(v2, v3);
+      *(u32x2*)((uint16_t*)ybase + (size_t)m * p.ldy + nc) = o;
+    } else {
+      f32x4 o = {v0, v1, v2, v3};
+      *(f32x4*)((float*)ybase + (size_t)m * p.ldy + nc) = o;
+    }
+  }
+}
+
 // XOR swizzle of 16-byte chunks inside a K-contiguous LDS row of KC chunks.
 // Any 8 consecutive rows (aligned to 8) reading the same logical chunk land in
 // 8 distinct 16-byte slots of a 128-byte bank line.
@@ -101,10 +145,15 @@ __device__ __forceinline__ int swz(int r) {
   return ((r / RPL) ^ ((r >> 3) & 3)) & (KC - 1);
 }
 
-// Swizzle of the 16-byte chunks of an NN B row (row = k).  The transpose read
-// of a 16-lane group touches 4 consecutive rows, 32 bytes each (chunks 2m,
-// 2m+1); XOR with 2*(k % 4) puts the 4 rows in distinct 32-byte slots.
-__device__ __forceinline__ int swz_nn(int k) { return (k & 3) << 1; }
+// Swizzle of the 16-byte chunks of an NN B row (row = k, NC chunks per row).
+// A transpose read is served 32 lanes at a time: two 16-lane groups that read
+// the same 4 consecutive rows, 32 bytes each, in adjacent 32-byte column slots
+// (2j, 2j+1).  XOR of the chunk index with 4*(k % 4) moves row k to slot
+// offset 2*(k % 4), so the 4 rows x 2 slots cover 8 distinct 32-byte slots:
+// all 64 banks, no conflict.  Rows of 8 chunks (tile_n = 64) have only 4
+// slots; there 2*(k % 4) keeps each 16-lane group conflict-free.
+template <int NC>
+__device__ __forceinline__ int swz_nn(int k) { return NC >= 16 ? (k & 3) << 2 : (k & 3) << 1; }
 
 // Linear workgroup id -> (tile_m, tile_n, partition).
 // Workgroups are dispatched round-robin over the 8 XCDs; with xcd_remap the
@@ -165,6 +214,9 @@ __device__ __forceinline__ void wait_vmcnt() {
   __builtin_amdgcn_s_waitcnt((N & 0xF) | ((N >> 4) << 14) | (0x7 << 4) | (0xF << 8));
 }
 
+// s_waitcnt lgkmcnt(0) (vmcnt and expcnt left at their maxima).
+__device__ __forceinline__ void wait_lgkmcnt0() { __builtin_amdgcn_s_waitcnt(0xF | (0x7 << 4) | (0x3 << 14)); }
+
 // 16 zero bytes: the DMA source of K-tail chunks, so every K tile issues the
 // same number of DMA loads (the vmcnt arithmetic below relies on it).
 static __device__ __attribute__((aligned(16))) const uint32_t g_zero16[4] = {0u, 0u, 0u, 0u};
@@ -186,12 +238,12 @@ struct GemmTile {
   static_assert((A_ELEMS * 2) % 1024 == 0 && (B_ELEMS * 2) % 1024 == 0, "tiles must be whole 1 KB blocks");
   static_assert(!NN || NC >= 8, "NN tiles need tile_n >= 64");
   static_assert(S >= 2 && S <= 5, "2..5 LDS stages");
-  // With more than two stages a wave waits for its oldest tile by count, so
-  // every wave must issue the same number of DMA loads per tile.
-  static_assert(S == 2 || (A_BLOCKS % NWAVES == 0 && B_BLOCKS % NWAVES == 0), "uneven DMA split");
+  // Waiting for one tile by count (vmcnt) needs every wave to issue the same
+  // number of DMA loads per tile; other splits wait for all loads.
+  static constexpr bool EVEN = A_BLOCKS % NWAVES == 0 && B_BLOCKS % NWAVES == 0;
   static constexpr int LPT = A_BLOCKS / NWAVES + B_BLOCKS / NWAVES;  // DMA loads per wave per tile
-  static_assert(S == 2 || LPT * (S - 2) <= 63, "vmcnt range");
-  static_assert(S == 2 || KS % 2 == 0, "cross-tile fragment prefetch needs an even number of k-steps");
+  static_assert(S == 2 || EVEN, "more than two stages need an even DMA split");
+  static_assert(!EVEN || LPT * (S - 1) <= 63, "vmcnt range");
 };
 
 template <int BM, int BN, int BK, int WM, int WN, int S, bool NN>
@@ -219,45 +271,63 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_bf16_kernel(GemmParams p) {
   // ---- global -> LDS ------------------------------------------------------
   // Wave w fills 1 KB blocks w, w + NWAVES, ...; lane l writes chunk l of its
   // block, fetching the global chunk that the swizzle assigns to that slot.
+  // Source pointers are formed once for tile 0 and stepped by a constant per
+  // tile; chunks past the end of the K range (last tile only) read 16 zero
+  // bytes instead, so every tile issues the same number of DMA loads.
+  constexpr int NA = (T::A_BLOCKS + T::NWAVES - 1) / T::NWAVES;
+  constexpr int NB = (T::B_BLOCKS + T::NWAVES - 1) / T::NWAVES;
   const int wave_s = __builtin_amdgcn_readfirstlane(wave);
   const uint32_t smem_base = lds_addr(smem);
-  auto load_tile = [&](int k0, int stage) {
-    const uint32_t a_lds = smem_base + (uint32_t)(stage * BUF * 2);
-    const uint32_t b_lds = a_lds + (uint32_t)(A_ELEMS * 2);
+  const int kspan = kend - kbeg;
+  const uint16_t* a_src[NA];
+  const uint16_t* b_src[NB];
+  int a_kofs[NA], b_kofs[NB];  // K offset of the lane's chunk inside a tile
 #pragma unroll
-    for (int j = 0; j < (T::A_BLOCKS + T::NWAVES - 1) / T::NWAVES; ++j) {
-      const int blk = wave_s + j * T::NWAVES;
-      if (T::A_BLOCKS % T::NWAVES != 0 && blk >= T::A_BLOCKS) break;
-      const int q = blk * 64 + lane;
+  for (int j = 0; j < NA; ++j) {
+    const int q = (wave_s + j * T::NWAVES) * 64 + lane;
+    const int row = q / KC, pc = q % KC;
+    const int lc = pc ^ swz<KC>(row);
+    int gr = m0 + row;
+    gr = gr < (int)p.M ? gr : (int)p.M - 1;
+    a_src[j] = p.a + (size_t)gr * p.lda + kbeg + lc * 8;
+    a_kofs[j] = lc * 8;
+  }
+#pragma unroll
+  for (int j = 0; j < NB; ++j) {
+    const int q = (wave_s + j * T::NWAVES) * 64 + lane;
+    if constexpr (!NN) {
       const int row = q / KC, pc = q % KC;
       const int lc = pc ^ swz<KC>(row);
-      int gr = m0 + row;
-      gr = gr < (int)p.M ? gr : (int)p.M - 1;
-      const int gk = k0 + lc * 8;
-      const void* src = gk < kend ? (const void*)(p.a + (size_t)gr * p.lda + gk) : (const void*)g_zero16;
+      int gr = n0 + row;
+      gr = gr < (int)p.N ? gr : (int)p.N - 1;
+      b_src[j] = p.b + (size_t)gr * p.ldb + kbeg + lc * 8;
+      b_kofs[j] = lc * 8;
+    } else {
+      const int row = q / NC, pc = q % NC;  // row = k within the tile
+      const int lc = pc ^ swz_nn<NC>(row);
+      int gn = n0 + lc * 8;
+      gn = gn < (int)p.N ? gn : (int)p.N - 8;
+      b_src[j] = p.b + (size_t)(kbeg + row) * p.ldb + gn;
+      b_kofs[j] = row;
+    }
+  }
+  const size_t b_step = NN ? (size_t)BK * p.ldb : (size_t)BK;
+  auto load_tile = [&](int t, int stage) {
+    const uint32_t a_lds = smem_base + (uint32_t)(stage * BUF * 2);
+    const uint32_t b_lds = a_lds + (uint32_t)(A_ELEMS * 2);
+    const int krem = kspan - t * BK;  // chunks at K offset >= krem are past the end
+#pragma unroll
+    for (int j = 0; j < NA; ++j) {
+      const int blk = wave_s + j * T::NWAVES;
+      if (T::A_BLOCKS % T::NWAVES != 0 && blk >= T::A_BLOCKS) break;
+      const void* src = a_kofs[j] < krem ? (const void*)(a_src[j] + (size_t)t * BK) : (const void*)g_zero16;
       lds_dma16(src, a_lds + blk * 1024);
     }
 #pragma unroll
-    for (int j = 0; j < (T::B_BLOCKS + T::NWAVES - 1) / T::NWAVES; ++j) {
+    for (int j = 0; j < NB; ++j) {
       const int blk = wave_s + j * T::NWAVES;
       if (T::B_BLOCKS % T::NWAVES != 0 && blk >= T::B_BLOCKS) break;
-      const int q = blk * 64 + lane;
-      const void* src;
-      if constexpr (!NN) {
-        const int row = q / KC, pc = q % KC;
-        const int lc = pc ^ swz<KC>(row);
-        int gr = n0 + row;
-        gr = gr < (int)p.N ? gr : (int)p.N - 1;
-        const int gk = k0 + lc * 8;
-        src = gk < kend ? (const void*)(p.b + (size_t)gr * p.ldb + gk) : (const void*)g_zero16;
-      } else {
-        const int row = q / NC, pc = q % NC;  // row = k within the tile
-        const int lc = pc ^ swz_nn(row);
-        int gn = n0 + lc * 8;
-        gn = gn < (int)p.N ? gn : (int)p.N - 8;
-        const int gk = k0 + row;
-        src = gk < kend ? (const void*)(p.b + (size_t)gk * p.ldb + gn) : (const void*)g_zero16;
-      }
+      const void* src = b_kofs[j] < krem ? (const void*)(b_src[j] + (size_t)t * b_step) : (const void*)g_zero16;
       lds_dma16(src, b_lds + blk * 1024);
     }
   };
@@ -280,7 +350,7 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_bf16_kernel(GemmParams p) {
   const int tg = lane >> 4, ti = lane & 15;
   const int nn_krow0 = 8 * (tg >> 1) + (ti >> 2);       // + ks*16 + 4*r
   const int nn_col0 = wn * TN + 16 * (tg & 1) + 4 * (ti & 3);  // + fn*32
-  const int nn_sw = swz_nn(nn_krow0);                   // (k & 3) is the same for every ks, r
+  const int nn_sw = swz_nn<NC>(nn_krow0);                   // (k & 3) is the same for every ks, r
 
   auto read_frags = [&](const uint16_t* As, int ks, bf16x8* xa, bf16x8* xb) {
     const uint16_t* Bs = As + A_ELEMS;
@@ -319,134 +389,113 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_bf16_kernel(GemmParams p) {
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc[fn][fm][r] = 0.0f;
 
-  // One K tile of MFMAs; the MFMAs of k-step ks overlap the LDS reads of ks + 1.
   // LDS instructions per k-step: FM b128 reads of A, FN b128 (NT) or 2*FN
   // transpose reads (NN) of B.
   constexpr int NREAD = FM + (NN ? 2 * FN : FN);
   constexpr int NMFMA = FM * FN;
-  auto compute_tile = [&](const uint16_t* As) {
-    bf16x8 xa[2][FM], xb[2][FN];
-    read_frags(As, 0, xa[0], xb[0]);
+  auto mfma_step = [&](const bf16x8* xa, const bf16x8* xb) {
 #pragma unroll
-    for (int ks = 0; ks < KS; ++ks) {
-      const int c = ks & 1;
-      if (ks + 1 < KS) read_frags(As, ks + 1, xa[c ^ 1], xb[c ^ 1]);
+    for (int fn = 0; fn < FN; ++fn)
 #pragma unroll
-      for (int fn = 0; fn < FN; ++fn)
-#pragma unroll
-        for (int fm = 0; fm < FM; ++fm)
-          acc[fn][fm] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(xb[c][fn], xa[c][fm], acc[fn][fm], 0, 0, 0);
-    }
-    // Instruction order for the scheduler: the reads of k-step 0, then each
-    // k-step's MFMAs with the next k-step's LDS reads slotted between them, so
-    // every fragment is requested a full k-step (NMFMA x 32 cycles) before use.
-    __builtin_amdgcn_sched_group_barrier(0x100, NREAD, 0);
-#pragma unroll
-    for (int ks = 0; ks + 1 < KS; ++ks) {
-#pragma unroll
-      for (int i = 0; i < NMFMA; ++i) {
-        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-        if (i < NREAD) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
-      }
-      if (NREAD > NMFMA) __builtin_amdgcn_sched_group_barrier(0x100, NREAD - NMFMA, 0);
-    }
-    __builtin_amdgcn_sched_group_barrier(0x008, NMFMA, 0);
+      for (int fm = 0; fm < FM; ++fm)
+        acc[fn][fm] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(xb[fn], xa[fm], acc[fn][fm], 0, 0, 0);
   };
-  // Ring of S stages: tile t lives in stage t % S.
+  // Scheduler hint for one k-step: its MFMAs with the LDS reads of the next
+  // k-step slotted between them, so each fragment is requested a full k-step
+  // (NMFMA x 32 cycles) before use.
+  auto interleave_hint = [&]() {
+#pragma unroll
+    for (int i = 0; i < NMFMA; ++i) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+      if (i < NREAD) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+    }
+    if (NREAD > NMFMA) __builtin_amdgcn_sched_group_barrier(0x100, NREAD - NMFMA, 0);
+  };
+
+  // Ring of S stages; tile t lives in stage t % S.  The prologue requests
+  // tiles 0 .. S-1.  In iteration `it` the wave runs k-steps 0 .. KS-2 of tile
+  // `it`, then waits for its own DMA of tile it+1 and meets the other waves at
+  // the barrier, which (a) publishes tile it+1 and (b) proves every wave has
+  // read all of stage it % S (the fragments of the last k-step are already in
+  // registers).  Stage it % S then receives tile it+S, and the first
+  // fragments of tile it+1 are read while the last k-step's MFMAs run, so the
+  // MFMA stream does not drain at tile boundaries.  Tiles it+1 .. it+S are in
+  // flight while tile `it` is computed.
+  // vmcnt arithmetic: with an even DMA split every wave issues LPT loads per
+  // tile, so "tile it+1 landed" is vmcnt <= LPT * (number of younger tiles in
+  // flight); otherwise, and near the end of K, the wave waits for all loads.
+  constexpr int LPT = T::LPT;
+  constexpr bool EVEN = T::EVEN;
+  bf16x8 xa[2][FM], xb[2][FN];
   if (nk > 0) {
 #pragma unroll
-    for (int t = 0; t < S - 1; ++t)
-      if (t < nk) load_tile(kbeg + t * BK, t);
-  }
-  if constexpr (S == 2) {
-    // Iteration `it` waits for its own tile, the barrier publishes every
-    // wave's DMA and frees the stage computed in iteration it-1, which then
-    // receives tile it+1.
-    for (int it = 0; it < nk; ++it) {
-      wait_vmcnt<0>();
-      __syncthreads();
-      if (it + 1 < nk) load_tile(kbeg + (it + 1) * BK, (it + 1) & 1);
-      compute_tile(smem + (it & 1) * BUF);
-    }
-  } else if (nk > 0) {
-    // S >= 3: the barrier of iteration `it` publishes tile it+1 (its DMA was
-    // issued S-2 iterations earlier), so the last k-step of tile `it` already
-    // reads the first fragments of tile it+1 and the MFMA stream does not
-    // drain at tile boundaries.  It also frees stage (it-1) % S, which receives
-    // tile it+S-1; tiles it+2 .. it+S-2 stay in flight.
-    // Tile 0 landed (own DMA): S-2 younger tiles may stay in flight, but only
-    // if all S-1 prologue tiles were issued (short K issues fewer).
-    if (nk >= S - 1)
-      wait_vmcnt<(S > 2 ? T::LPT * (S - 2) : 0)>();
+    for (int t = 0; t < S; ++t)
+      if (t < nk) load_tile(t, t);
+    if (EVEN && nk >= S)
+      wait_vmcnt<EVEN ? LPT * (S - 1) : 0>();
     else
       wait_vmcnt<0>();
     __syncthreads();
-    bf16x8 xa[2][FM], xb[2][FN];
     read_frags(smem, 0, xa[0], xb[0]);
-    for (int it = 0; it < nk; ++it) {
-      if (it + S - 2 < nk)
-        wait_vmcnt<(S > 2 ? T::LPT * (S - 3) : 0)>();  // tile it+1 landed
+  }
+  constexpr int CL = (KS - 1) & 1;  // fragment buffer of the last k-step
+  // One iteration; BARRIER: not the last tile; LOAD: tile it+S exists.  The
+  // three loop copies below keep each body free of branches, so the compiler's
+  // LDS wait counts never merge the next tile's reads into the current ones.
+  auto iteration = [&](int it, auto barrier_c, auto load_c) {
+    constexpr bool BARRIER = decltype(barrier_c)::value, LOAD = decltype(load_c)::value;
+    const uint16_t* cur = smem + (it % S) * BUF;
+#pragma unroll
+    for (int ks = 0; ks + 1 < KS; ++ks) {
+      const int c = ks & 1;
+      read_frags(cur, ks + 1, xa[c ^ 1], xb[c ^ 1]);
+      mfma_step(xa[c], xb[c]);
+      interleave_hint();
+    }
+    if constexpr (BARRIER) {
+      if constexpr (LOAD && EVEN)
+        wait_vmcnt<EVEN ? LPT * (S - 2) : 0>();  // tile it+1 landed, it+2 .. it+S-1 may fly
       else
         wait_vmcnt<0>();
+      wait_lgkmcnt0();  // this wave's reads of stage it % S are complete
       __syncthreads();
-      if (it + S - 1 < nk) load_tile(kbeg + (it + S - 1) * BK, (it + S - 1) % S);
-      const uint16_t* cur = smem + (it % S) * BUF;
-      const uint16_t* nxt = smem + ((it + 1) % S) * BUF;
-      const bool more = it + 1 < nk;
-#pragma unroll
-      for (int ks = 0; ks < KS; ++ks) {
-        const int c = ks & 1;  // KS is even, so every tile starts in buffer 0
-        if (ks + 1 < KS)
-          read_frags(cur, ks + 1, xa[c ^ 1], xb[c ^ 1]);
-        else if (more)
-          read_frags(nxt, 0, xa[c ^ 1], xb[c ^ 1]);
-#pragma unroll
-        for (int fn = 0; fn < FN; ++fn)
-#pragma unroll
-          for (int fm = 0; fm < FM; ++fm)
-            acc[fn][fm] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(xb[c][fn], xa[c][fm], acc[fn][fm], 0, 0, 0);
-      }
+      if constexpr (LOAD) load_tile(it + S, it % S);
+      read_frags(smem + ((it + 1) % S) * BUF, 0, xa[CL ^ 1], xb[CL ^ 1]);
     }
-  }
+    mfma_step(xa[CL], xb[CL]);
+    if constexpr (BARRIER) interleave_hint();
+    if constexpr (CL == 0) {
+      // Odd KS: tile it+1 starts in buffer 0.
+#pragma unroll
+      for (int f = 0; f < FM; ++f) xa[0][f] = xa[1][f];
+#pragma unroll
+      for (int f = 0; f < FN; ++f) xb[0][f] = xb[1][f];
+    }
+  };
+  using True = std::integral_constant<bool, true>;
+  using False = std::integral_constant<bool, false>;
+  int it = 0;
+  for (; it + S < nk; ++it) iteration(it, True{}, True{});
+  for (; it + 1 < nk; ++it) iteration(it, True{}, False{});
+  if (it < nk) iteration(it, False{}, False{});
 
   // Epilogue.  Lane l of block (fn, fm) holds C[m][n] for
   //   m = fm*32 + (l & 31),  n = fn*32 + 8*g + 4*(l >> 5) + {0..3},  g = 0..3,
   // i.e. four consecutive columns per (lane, g): one 16-byte (f32) or
-  // 8-byte (bf16) store.
+  // 8-byte (bf16) store.  The (fm, fn) loops are expanded at compile time so
+  // acc is only ever indexed by constants and stays in registers.
   const bool partial_plane = p.split_k > 1;
   char* ybase = (char*)p.y + (partial_plane ? (size_t)part * p.y_split_stride : 0);
-#pragma unroll
-  for (int fm = 0; fm < FM; ++fm) {
+  static_for<FM>([&](auto fmc) {
+    constexpr int fm = decltype(fmc)::value;
     const int m = m0 + wm * TM + fm * 32 + lrow;
-    if (m >= (int)p.M) continue;
-#pragma unroll
-    for (int fn = 0; fn < FN; ++fn) {
-#pragma unroll
-      for (int g = 0; g < 4; ++g) {
-        const int n = n0 + wn * TN + fn * 32 + g * 8 + lhalf * 4;
-        if (n >= (int)p.N) continue;
-        float v0 = acc[fn][fm][g * 4 + 0], v1 = acc[fn][fm][g * 4 + 1];
-        float v2 = acc[fn][fm][g * 4 + 2], v3 = acc[fn][fm][g * 4 + 3];
-        if (!partial_plane && p.epi.n) {
-          f32x4 bv = {0.0f, 0.0f, 0.0f, 0.0f};
-          if (p.bias) bv = f32x4{p.bias[n], p.bias[n + 1], p.bias[n + 2], p.bias[n + 3]};
-          v0 = epi_apply(v0, bv.x, p.epi);
-          v1 = epi_apply(v1, bv.y, p.epi);
-          v2 = epi_apply(v2, bv.z, p.epi);
-          v3 = epi_apply(v3, bv.w, p.epi);
-        }
-        if (!partial_plane && p.out_bf16) {
-          u32x2 o;
-          o.x = (uint32_t)f32_to_bf16_rne(v0) | ((uint32_t)f32_to_bf16_rne(v1) << 16);
-          o.y = (uint32_t)f32_to_bf16_rne(v2) | ((uint32_t)f32_to_bf16_rne(v3) << 16);
-          *(u32x2*)((uint16_t*)ybase + (size_t)m * p.ldy + n) = o;
-        } else {
-          f32x4 o = {v0, v1, v2, v3};
-          *(f32x4*)((float*)ybase + (size_t)m * p.ldy + n) = o;
-        }
-      }
+    if (m < (int)p.M) {
+      static_for<FN>([&](auto fnc) {
+        constexpr int fn = decltype(fnc)::value;
+        store_block(p, acc[fn][fm], ybase, m, n0 + wn * TN + fn * 32 + lhalf * 4, partial_plane);
+      });
     }
-  }
+  });
 }
 
 }  // namespace t0mi
