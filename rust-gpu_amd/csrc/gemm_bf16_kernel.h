@@ -272,8 +272,9 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_bf16_kernel(GemmParams p) {
   // Wave w fills 1 KB blocks w, w + NWAVES, ...; lane l writes chunk l of its
   // block, fetching the global chunk that the swizzle assigns to that slot.
   // Source pointers are formed once for tile 0 and stepped by a constant per
-  // tile; chunks past the end of the K range (last tile only) read 16 zero
-  // bytes instead, so every tile issues the same number of DMA loads.
+  // tile; chunks past the end of the K range (last tile only, checked only
+  // when that tile is loaded) read 16 zero bytes instead, so every tile issues
+  // the same number of DMA loads.
   constexpr int NA = (T::A_BLOCKS + T::NWAVES - 1) / T::NWAVES;
   constexpr int NB = (T::B_BLOCKS + T::NWAVES - 1) / T::NWAVES;
   const int wave_s = __builtin_amdgcn_readfirstlane(wave);
@@ -312,6 +313,27 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_bf16_kernel(GemmParams p) {
     }
   }
   const size_t b_step = NN ? (size_t)BK * p.ldb : (size_t)BK;
+  // DMA load j of tile t (j < NA: A block, else B block) into `stage`.
+  // CHECK: the tile may end past the K range (only the last tile can).
+  auto dma_one = [&](int t, int stage, auto jc, auto check_c) {
+    constexpr int j = decltype(jc)::value;
+    constexpr bool CHECK = decltype(check_c)::value;
+    const uint32_t a_lds = smem_base + (uint32_t)(stage * BUF * 2);
+    const int krem = kspan - t * BK;
+    if constexpr (j < NA) {
+      const int blk = wave_s + j * T::NWAVES;
+      if (T::A_BLOCKS % T::NWAVES != 0 && blk >= T::A_BLOCKS) return;
+      const void* src = a_src[j] + (size_t)t * BK;
+      if (CHECK && a_kofs[j] >= krem) src = g_zero16;
+      lds_dma16(src, a_lds + blk * 1024);
+    } else {
+      const int blk = wave_s + (j - NA) * T::NWAVES;
+      if (T::B_BLOCKS % T::NWAVES != 0 && blk >= T::B_BLOCKS) return;
+      const void* src = b_src[j - NA] + (size_t)t * b_step;
+      if (CHECK && b_kofs[j - NA] >= krem) src = g_zero16;
+      lds_dma16(src, a_lds + (uint32_t)(A_ELEMS * 2) + blk * 1024);
+    }
+  };
   auto load_tile = [&](int t, int stage) {
     const uint32_t a_lds = smem_base + (uint32_t)(stage * BUF * 2);
     const uint32_t b_lds = a_lds + (uint32_t)(A_ELEMS * 2);
@@ -352,6 +374,33 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_bf16_kernel(GemmParams p) {
   const int nn_col0 = wn * TN + 16 * (tg & 1) + 4 * (ti & 3);  // + fn*32
   const int nn_sw = swz_nn<NC>(nn_krow0);                   // (k & 3) is the same for every ks, r
 
+  // LDS read r of k-step ks (r < FM: A fragment r; then B: fragment r - FM
+  // (NT), or transpose half (r - FM) % 2 of fragment (r - FM) / 2 (NN)).
+  i16x4 trh[FN][2];
+  auto read_one = [&](const uint16_t* As, int ks, auto rc, bf16x8* xa, bf16x8* xb) {
+    constexpr int r = decltype(rc)::value;
+    const uint16_t* Bs = As + A_ELEMS;
+    if constexpr (r < FM) {
+      xa[r] = *(const bf16x8*)(As + a_off[ks] + r * 32 * BK);
+    } else if constexpr (!NN) {
+      xb[r - FM] = *(const bf16x8*)(Bs + b_off[ks] + (r - FM) * 32 * BK);
+    } else {
+      constexpr int fn = (r - FM) / 2, h = (r - FM) % 2;
+      const int col = nn_col0 + fn * 32;
+      const int eoff = (((col >> 3) ^ nn_sw) << 3) + (col & 4);
+      const int krow = ks * 16 + 4 * h + nn_krow0;
+      trh[fn][h] = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+          (__attribute__((address_space(3))) i16x4*)(Bs + krow * BN + eoff));
+      if constexpr (h == 1) {
+        u32x4 u;
+        u.x = (uint32_t)(uint16_t)trh[fn][0].x | ((uint32_t)(uint16_t)trh[fn][0].y << 16);
+        u.y = (uint32_t)(uint16_t)trh[fn][0].z | ((uint32_t)(uint16_t)trh[fn][0].w << 16);
+        u.z = (uint32_t)(uint16_t)trh[fn][1].x | ((uint32_t)(uint16_t)trh[fn][1].y << 16);
+        u.w = (uint32_t)(uint16_t)trh[fn][1].z | ((uint32_t)(uint16_t)trh[fn][1].w << 16);
+        xb[fn] = __builtin_bit_cast(bf16x8, u);
+      }
+    }
+  };
   auto read_frags = [&](const uint16_t* As, int ks, bf16x8* xa, bf16x8* xb) {
     const uint16_t* Bs = As + A_ELEMS;
 #pragma unroll
@@ -393,6 +442,7 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_bf16_kernel(GemmParams p) {
   // transpose reads (NN) of B.
   constexpr int NREAD = FM + (NN ? 2 * FN : FN);
   constexpr int NMFMA = FM * FN;
+  constexpr int NDMA = NA + NB;  // DMA loads per wave per tile (some may be idle)
   auto mfma_step = [&](const bf16x8* xa, const bf16x8* xb) {
 #pragma unroll
     for (int fn = 0; fn < FN; ++fn)
@@ -442,7 +492,7 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_bf16_kernel(GemmParams p) {
   // One iteration; BARRIER: not the last tile; LOAD: tile it+S exists.  The
   // three loop copies below keep each body free of branches, so the compiler's
   // LDS wait counts never merge the next tile's reads into the current ones.
-  auto iteration = [&](int it, auto barrier_c, auto load_c) {
+  auto iteration = [&](int it, auto barrier_c, auto load_c, auto check_c) {
     constexpr bool BARRIER = decltype(barrier_c)::value, LOAD = decltype(load_c)::value;
     const uint16_t* cur = smem + (it % S) * BUF;
 #pragma unroll
@@ -459,11 +509,26 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_bf16_kernel(GemmParams p) {
         wait_vmcnt<0>();
       wait_lgkmcnt0();  // this wave's reads of stage it % S are complete
       __syncthreads();
-      if constexpr (LOAD) load_tile(it + S, it % S);
-      read_frags(smem + ((it + 1) % S) * BUF, 0, xa[CL ^ 1], xb[CL ^ 1]);
+      // The last k-step's MFMAs with the DMA loads of tile it+S and the reads
+      // of tile it+1's first k-step placed one per MFMA, in this order (the
+      // scheduler may not move anything across the sched_barriers).
+      const uint16_t* nxt = smem + ((it + 1) % S) * BUF;
+      constexpr int NMEM = NDMA > NREAD ? NDMA : NREAD;
+      constexpr int NSLOT = NMFMA > NMEM ? NMFMA : NMEM;
+      static_for<NSLOT>([&](auto ic) {
+        constexpr int i = decltype(ic)::value;
+        if constexpr (i < NMFMA) {
+          constexpr int fn = i / FM, fm = i % FM;
+          acc[fn][fm] =
+              __builtin_amdgcn_mfma_f32_32x32x16_bf16(xb[CL][fn], xa[CL][fm], acc[fn][fm], 0, 0, 0);
+        }
+        if constexpr (LOAD && i < NDMA) dma_one(it + S, it % S, std::integral_constant<int, i>{}, check_c);
+        if constexpr (i < NREAD) read_one(nxt, 0, std::integral_constant<int, i>{}, xa[CL ^ 1], xb[CL ^ 1]);
+        __builtin_amdgcn_sched_barrier(0);
+      });
+    } else {
+      mfma_step(xa[CL], xb[CL]);
     }
-    mfma_step(xa[CL], xb[CL]);
-    if constexpr (BARRIER) interleave_hint();
     if constexpr (CL == 0) {
       // Odd KS: tile it+1 starts in buffer 0.
 #pragma unroll
@@ -474,10 +539,12 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_bf16_kernel(GemmParams p) {
   };
   using True = std::integral_constant<bool, true>;
   using False = std::integral_constant<bool, false>;
+  const int nfull = kspan / BK;  // tiles that end inside the K range
   int it = 0;
-  for (; it + S < nk; ++it) iteration(it, True{}, True{});
-  for (; it + 1 < nk; ++it) iteration(it, True{}, False{});
-  if (it < nk) iteration(it, False{}, False{});
+  for (; it + S < nfull; ++it) iteration(it, True{}, True{}, False{});  // steady state
+  for (; it + S < nk; ++it) iteration(it, True{}, True{}, True{});      // loads the partial last tile
+  for (; it + 1 < nk; ++it) iteration(it, True{}, False{}, False{});
+  if (it < nk) iteration(it, False{}, False{}, False{});
 
   // Epilogue.  Lane l of block (fn, fm) holds C[m][n] for
   //   m = fm*32 + (l & 31),  n = fn*32 + 8*g + 4*(l >> 5) + {0..3},  g = 0..3,
