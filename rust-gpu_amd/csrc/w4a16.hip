@@ -21,48 +21,12 @@
 #include <string.h>
 
 #include "t0mi_ctx.h"
+#include "w4a16_decode.h"
 #include "w4a16_prefill.h"
 
 using namespace t0mi;
 
 namespace t0mi {
-
-typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
-
-struct W4Params {
-  const uint16_t* a;       // [M, K] bf16
-  const uint32_t* w;       // [K/8, N] packed int4
-  const uint16_t* scales;  // [K/g, N] bf16
-  const uint32_t* zeros;   // [K/g, N/8] packed int4, or null -> zp_const
-  void* y;                 // [M, N] out (or f32 partial planes)
-  uint32_t M, K, N, group; // group % 32 == 0
-  uint32_t zp_const;
-  uint32_t out_bf16;
-  uint32_t kb_per_split;   // k-blocks (of 32) per grid.y partition
-  uint64_t y_split_stride; // bytes between partial planes when gridDim.y > 1
-};
-
-__device__ __forceinline__ bf16x8_t nib_pairs(uint32_t w) {
-  // 8 nibbles -> bf16 (128+q) in element order q0,q4,q1,q5,q2,q6,q3,q7.
-  u32x4 d;
-  d.x = (w & 0x000F000Fu) | 0x43004300u;
-  d.y = ((w >> 4) & 0x000F000Fu) | 0x43004300u;
-  d.z = ((w >> 8) & 0x000F000Fu) | 0x43004300u;
-  d.w = ((w >> 12) & 0x000F000Fu) | 0x43004300u;
-  return __builtin_bit_cast(bf16x8_t, d);
-}
-
-__device__ __forceinline__ bf16x8_t perm_act(u32x4 a) {
-  // a = (a0,a1)(a2,a3)(a4,a5)(a6,a7) -> (a0,a4)(a1,a5)(a2,a6)(a3,a7)
-  u32x4 o;
-  o.x = __builtin_amdgcn_perm(a.z, a.x, 0x05040100u);
-  o.y = __builtin_amdgcn_perm(a.z, a.x, 0x07060302u);
-  o.z = __builtin_amdgcn_perm(a.w, a.y, 0x05040100u);
-  o.w = __builtin_amdgcn_perm(a.w, a.y, 0x07060302u);
-  return __builtin_bit_cast(bf16x8_t, o);
-}
-
-__device__ __forceinline__ float bf16f(uint32_t h) { return __builtin_bit_cast(float, h << 16); }
 
 // Decode kernel: M <= 16 rows per slab.  One workgroup = WAVES waves on one
 // 64-column strip; wave v takes k-blocks [kb0 + v*KBW, +KBW) of this grid.y
@@ -374,6 +338,8 @@ extern "C" int t0mi_w4a16_gemm(t0mi_ctx* ctx, uint64_t a, uint64_t qweight, uint
   p.group = group;
   p.zp_const = zp_const;
   p.out_bf16 = out_dtype == T0MI_OUT_BF16;
+  p.nib_mask = 0x000F000Fu;
+  p.nib_magic = 0x43004300u;
   if (m > kDecodeMaxRows && (group & (group - 1)) == 0) {
     // Many rows: dequant fused into the MFMA K-loop, weights read once per tile column.
     W4PrefillParams q;
@@ -410,10 +376,20 @@ extern "C" int t0mi_w4a16_gemm(t0mi_ctx* ctx, uint64_t a, uint64_t qweight, uint
     hipError_t e = hipGetLastError();
     return e == hipSuccess ? T0MI_OK : hip_fail(e, "w4a16 prefill launch");
   }
-  constexpr int WAVES = 8, KBW = 16;
+  // Decode: 64-column strips; groups of 32..256 K run the v2 kernel (16-wave
+  // workgroups of 8 k-blocks per wave), other groups the generic kernel.
+  const bool v2 = group == 32 || group == 64 || group == 128 || group == 256;
+  constexpr int KBW2 = 8;
+  constexpr int WAVES = 8, KBW = 16;  // generic kernel
   const uint32_t kb_tot = k / 32;
-  const uint32_t ky = (kb_tot + WAVES * KBW - 1) / (WAVES * KBW);
-  p.kb_per_split = WAVES * KBW;
+  uint32_t nw2 = 16;
+  if (v2) {
+    const uint32_t waves_needed = (kb_tot + KBW2 - 1) / KBW2;
+    nw2 = waves_needed <= 4 ? 4 : (waves_needed <= 8 ? 8 : 16);
+  }
+  const uint32_t per_part = v2 ? nw2 * KBW2 : WAVES * KBW;
+  const uint32_t ky = (kb_tot + per_part - 1) / per_part;
+  p.kb_per_split = per_part;
   const uint32_t strips = (n + 63) / 64;
   // Row slabs of 16: the decode kernel is launched once per slab.
   for (uint32_t r0 = 0; r0 < m; r0 += 16) {
@@ -430,24 +406,40 @@ extern "C" int t0mi_w4a16_gemm(t0mi_ctx* ctx, uint64_t a, uint64_t qweight, uint
     } else {
       p.y = (char*)y + (size_t)r0 * n * ob;
     }
-    const dim3 grid(strips, ky), block(WAVES * 64);
     const bool z = qzeros != 0;
-    switch (group) {
-#define T0MI_W4_CASE(G)                                                                                    \
-  case G:                                                                                                  \
-    if (z)                                                                                                 \
-      hipLaunchKernelGGL((w4a16_decode_grouped<WAVES, KBW, G / 32, true>), grid, block, 0, ctx->stream, p);  \
-    else                                                                                                   \
-      hipLaunchKernelGGL((w4a16_decode_grouped<WAVES, KBW, G / 32, false>), grid, block, 0, ctx->stream, p); \
-    break;
-      T0MI_W4_CASE(32)
-      T0MI_W4_CASE(64)
-      T0MI_W4_CASE(128)
-      T0MI_W4_CASE(256)
-      T0MI_W4_CASE(512)
-#undef T0MI_W4_CASE
-      default:  // groups spanning several waves' K ranges
+    if (v2) {
+      const dim3 grid(strips, ky), block(nw2 * 64);
+#define T0MI_W4_V2(NW, G)                                                                                      \
+  if (z)                                                                                                       \
+    hipLaunchKernelGGL((w4a16_decode_v2<NW, KBW2, G / 32, true>), grid, block, 0, ctx->stream, p);           \
+  else                                                                                                         \
+    hipLaunchKernelGGL((w4a16_decode_v2<NW, KBW2, G / 32, false>), grid, block, 0, ctx->stream, p);
+#define T0MI_W4_V2_G(NW)                                                                                       \
+  switch (group) {                                                                                             \
+    case 32: T0MI_W4_V2(NW, 32) break;                                                                         \
+    case 64: T0MI_W4_V2(NW, 64) break;                                                                         \
+    case 128: T0MI_W4_V2(NW, 128) break;                                                                       \
+    default: T0MI_W4_V2(NW, 256) break;                                                                        \
+  }
+      if (nw2 == 4) {
+        T0MI_W4_V2_G(4)
+      } else if (nw2 == 8) {
+        T0MI_W4_V2_G(8)
+      } else {
+        T0MI_W4_V2_G(16)
+      }
+#undef T0MI_W4_V2_G
+#undef T0MI_W4_V2
+    } else {
+      const dim3 grid(strips, ky), block(WAVES * 64);
+      if (group == 512) {
+        if (z)
+          hipLaunchKernelGGL((w4a16_decode_grouped<WAVES, KBW, 16, true>), grid, block, 0, ctx->stream, p);
+        else
+          hipLaunchKernelGGL((w4a16_decode_grouped<WAVES, KBW, 16, false>), grid, block, 0, ctx->stream, p);
+      } else {  // groups spanning several waves' K ranges
         hipLaunchKernelGGL((w4a16_decode_kernel<WAVES, KBW>), grid, block, 0, ctx->stream, p);
+      }
     }
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return hip_fail(e, "w4a16 launch");

@@ -1,0 +1,216 @@
+// w4a16_decode.h — gfx950 W4A16 decode GEMM (M <= 16 rows per launch slab).
+//
+// Y[M,N] = A[M,K] . W[K,N] with W stored as INT4 nibbles (u32 [K/8][N]; word
+// (kk, n) holds q[8kk+e][n] in bits 4e..4e+3, the reference's low-nibble-first
+// order, src/t0/quant_kernels.rs:3-10), one bf16 scale per `group` K values and
+// column, and a zero point per group and column (packed u32 [K/g][N/8]) or a
+// constant.  w = (q - z) * s exactly as the reference defines it
+// (quant_kernels.rs:24, 95-100); the reference itself has no fused kernel.
+//
+// Exact dequant inside the MFMA: (0x43004300 | (w >> 4j) & 0x000F000F) is the
+// bf16 pair (128 + q_j, 128 + q_{j+4}), exact integers, so per group and column
+//     P = sum_k a_k (128 + q_k),   S = sum_k a_k   (an MFMA against ones)
+//     y += s * (P - (128 + z) * S)                  == sum_k a_k (q_k - z) s
+// with the activation operand permuted into the same k order as the pairs.
+//
+// Memory plan (HBM-bound: 0.5 B per weight): a workgroup owns a 64-column
+// strip; each of its NW waves owns KBW consecutive 32-K blocks and issues all
+// of its 16-byte weight loads (non-temporal, one 1 KB row segment per
+// instruction), activation loads and scale/zero loads before any compute, so a
+// CU keeps NW * KBW KB of weights in flight; blocks are then dequantized and
+// multiplied in arrival order.  The waves' [16 x 64] fp32 partials are summed
+// through LDS in wave order (deterministic) and stored as 8-byte bf16 (16-byte
+// f32) row segments.
+#pragma once
+#include "gemm_bf16_kernel.h"
+
+namespace t0mi {
+
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+
+struct W4Params {
+  const uint16_t* a;       // [M, K] bf16
+  const uint32_t* w;       // [K/8, N] packed int4
+  const uint16_t* scales;  // [K/g, N] bf16
+  const uint32_t* zeros;   // [K/g, N/8] packed int4, or null -> zp_const
+  void* y;                 // [M, N] out (or f32 partial planes)
+  uint32_t M, K, N, group; // group % 32 == 0
+  uint32_t zp_const;
+  uint32_t out_bf16;
+  uint32_t kb_per_split;   // k-blocks (of 32) per grid.y partition
+  uint64_t y_split_stride; // bytes between partial planes when gridDim.y > 1
+  uint32_t nib_mask;       // 0x000F000F (see nib_pairs_ao)
+  uint32_t nib_magic;      // 0x43004300
+};
+
+__device__ __forceinline__ bf16x8_t nib_pairs(uint32_t w) {
+  // 8 nibbles -> bf16 (128+q) in element order q0,q4,q1,q5,q2,q6,q3,q7.
+  u32x4 d;
+  d.x = (w & 0x000F000Fu) | 0x43004300u;
+  d.y = ((w >> 4) & 0x000F000Fu) | 0x43004300u;
+  d.z = ((w >> 8) & 0x000F000Fu) | 0x43004300u;
+  d.w = ((w >> 12) & 0x000F000Fu) | 0x43004300u;
+  return __builtin_bit_cast(bf16x8_t, d);
+}
+
+// nib_pairs in 7 VALU instructions (3 shifts, 4 v_bfi_b32): with mask =
+// 0x000F000F and magic = 0x43004300 (disjoint bits), (mask & x) | (~mask & magic)
+// is (x & mask) | magic, the bit-field-insert form.  Both arrive as kernel
+// arguments so that they stay in registers instead of folding into literals
+// (a gfx9 VOP3 instruction takes no literal operand).
+__device__ __forceinline__ uint32_t bfi(uint32_t mask, uint32_t x, uint32_t y) { return (mask & x) | (~mask & y); }
+__device__ __forceinline__ bf16x8_t nib_pairs_ao(uint32_t w, uint32_t mask, uint32_t magic) {
+  u32x4 d;
+  d.x = bfi(mask, w, magic);
+  d.y = bfi(mask, w >> 4, magic);
+  d.z = bfi(mask, w >> 8, magic);
+  d.w = bfi(mask, w >> 12, magic);
+  return __builtin_bit_cast(bf16x8_t, d);
+}
+
+__device__ __forceinline__ bf16x8_t perm_act(u32x4 a) {
+  // a = (a0,a1)(a2,a3)(a4,a5)(a6,a7) -> (a0,a4)(a1,a5)(a2,a6)(a3,a7)
+  u32x4 o;
+  o.x = __builtin_amdgcn_perm(a.z, a.x, 0x05040100u);
+  o.y = __builtin_amdgcn_perm(a.z, a.x, 0x07060302u);
+  o.z = __builtin_amdgcn_perm(a.w, a.y, 0x05040100u);
+  o.w = __builtin_amdgcn_perm(a.w, a.y, 0x07060302u);
+  return __builtin_bit_cast(bf16x8_t, o);
+}
+
+__device__ __forceinline__ float bf16f(uint32_t h) { return __builtin_bit_cast(float, h << 16); }
+
+// One workgroup = NW waves on one 64-column strip; wave v of partition
+// blockIdx.y owns k-blocks [kb0, kb0 + KBW), kb0 = (blockIdx.y * NW + v) * KBW.
+// Groups are KBPG k-blocks (KBPG | KBW), so every wave covers whole groups and
+// K % group == 0 makes every group either complete or absent: absent groups
+// (the ragged end of K) are skipped by a wave-uniform branch and their loads
+// read a clamped, valid address.  Lane (c, g) = (lane % 16, lane / 16) loads
+// the 4 words of columns n0 + 4c .. +3 for K sub-row g of each block and
+// activation row c (rows >= M read row 0 and are never stored).
+template <int NW, int KBW, int KBPG, bool ZEROS>
+__global__ __launch_bounds__(NW * 64) void w4a16_decode_v2(W4Params p) {
+  static_assert(KBW % KBPG == 0, "whole groups per wave");
+  constexpr int NG = KBW / KBPG;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int c = lane & 15, g = lane >> 4;
+  const int n0 = blockIdx.x * 64;
+  const int ncol = n0 + 4 * c;
+  const bool col_ok = ncol < (int)p.N;  // N % 8 == 0, so the whole quad is in range
+  const int ncol_c = col_ok ? ncol : 0;
+  const int kb_tot = (int)(p.K / 32);
+  const int kb0 = __builtin_amdgcn_readfirstlane(((int)blockIdx.y * NW + wave) * KBW);
+  int nkb = kb_tot - kb0;  // valid k-blocks of this wave (wave-uniform)
+  nkb = nkb < 0 ? 0 : (nkb > KBW ? KBW : nkb);
+  const int arow = c < (int)p.M ? c : 0;
+
+  const int ngroups = kb_tot / KBPG;
+  const uint32_t mask = p.nib_mask, magic = p.nib_magic;
+  const bf16x8_t ones = __builtin_bit_cast(bf16x8_t, (u32x4){0x3F803F80u, 0x3F803F80u, 0x3F803F80u, 0x3F803F80u});
+  f32x4 acc[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) acc[j] = (f32x4){0.f, 0.f, 0.f, 0.f};
+
+  // FULL: all KBW blocks of the wave exist (every wave but those at the ragged
+  // end of K); then nothing is clamped or skipped and no branch separates the
+  // loads from their uses.
+  auto body = [&](auto full_c) {
+    constexpr bool FULL = decltype(full_c)::value;
+    u32x4 wv[KBW], av[KBW];
+    u32x2 sv[NG];
+    uint32_t zv[NG];
+    // Activations (L2-resident) and scales first, weights last: loads complete
+    // in issue order, so block b's dequant waits only for weight row b.
+#pragma unroll
+    for (int b = 0; b < KBW; ++b) {
+      int kb = kb0 + b;
+      if (!FULL) kb = kb < kb_tot ? kb : kb_tot - 1;
+      av[b] = *(const u32x4*)(p.a + (size_t)arow * p.K + kb * 32 + g * 8);
+    }
+#pragma unroll
+    for (int q = 0; q < NG; ++q) {
+      int grp = kb0 / KBPG + q;
+      if (!FULL) grp = grp < ngroups ? grp : ngroups - 1;
+      sv[q] = *(const u32x2*)(p.scales + (size_t)grp * p.N + ncol_c);
+      zv[q] = ZEROS ? p.zeros[(size_t)grp * (p.N / 8) + ncol_c / 8] : 0u;  // shifted at use
+    }
+#pragma unroll
+    for (int b = 0; b < KBW; ++b) {
+      int kb = kb0 + b;
+      if (!FULL) kb = kb < kb_tot ? kb : kb_tot - 1;
+      wv[b] = __builtin_nontemporal_load((const u32x4*)(p.w + (size_t)(kb * 4 + g) * p.N + ncol_c));
+    }
+    // Every load is issued before the first dequant: nothing may move across.
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int q = 0; q < NG; ++q) {
+      if (!FULL && q * KBPG >= nkb) break;  // wave-uniform: the ragged end of K
+      f32x4 P[4], S = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int j = 0; j < 4; ++j) P[j] = (f32x4){0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int i = 0; i < KBPG; ++i) {
+        const int b = q * KBPG + i;
+        const bf16x8_t A = perm_act(av[b]);
+        S = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A, ones, S, 0, 0, 0);
+        P[0] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A, nib_pairs_ao(wv[b].x, mask, magic), P[0], 0, 0, 0);
+        P[1] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A, nib_pairs_ao(wv[b].y, mask, magic), P[1], 0, 0, 0);
+        P[2] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A, nib_pairs_ao(wv[b].z, mask, magic), P[2], 0, 0, 0);
+        P[3] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A, nib_pairs_ao(wv[b].w, mask, magic), P[3], 0, 0, 0);
+      }
+      // y += s * (P - (128 + z) * S) for the four columns ncol + j of this lane.
+      const float s4[4] = {bf16f(sv[q].x & 0xFFFFu), bf16f(sv[q].x >> 16), bf16f(sv[q].y & 0xFFFFu),
+                           bf16f(sv[q].y >> 16)};
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const float z = 128.0f + (float)(ZEROS ? ((zv[q] >> (4 * ((ncol_c & 7) + j))) & 0xFu) : p.zp_const);
+        acc[j].x = fmaf(s4[j], fmaf(-z, S.x, P[j].x), acc[j].x);
+        acc[j].y = fmaf(s4[j], fmaf(-z, S.y, P[j].y), acc[j].y);
+        acc[j].z = fmaf(s4[j], fmaf(-z, S.z, P[j].z), acc[j].z);
+        acc[j].w = fmaf(s4[j], fmaf(-z, S.w, P[j].w), acc[j].w);
+      }
+    }
+  };
+  if (nkb == KBW)
+    body(std::integral_constant<bool, true>{});
+  else
+    body(std::integral_constant<bool, false>{});
+
+  // Lane (c, g) holds rows 4g + r, columns 4c + j as acc[j][r].  Stage them as
+  // red[wave][row][col] so that each of 256 threads sums one row segment of
+  // 4 columns over the waves (in wave order) and stores it with one vector store.
+  __shared__ __attribute__((aligned(16))) float red[NW * 16 * 64];
+  float* mine = red + wave * 16 * 64;
+#pragma unroll
+  for (int r = 0; r < 4; ++r)
+    *(f32x4*)(mine + (4 * g + r) * 64 + 4 * c) = (f32x4){acc[0][r], acc[1][r], acc[2][r], acc[3][r]};
+  __syncthreads();
+  for (int t = threadIdx.x; t < 256; t += NW * 64) {
+    const int R = t >> 4, C = t & 15;
+    f32x4 s4 = *(const f32x4*)(red + R * 64 + 4 * C);
+#pragma unroll
+    for (int v = 1; v < NW; ++v) {
+      const f32x4 t4 = *(const f32x4*)(red + (v * 16 + R) * 64 + 4 * C);
+      s4.x += t4.x;
+      s4.y += t4.y;
+      s4.z += t4.z;
+      s4.w += t4.w;
+    }
+    const int col = n0 + 4 * C;
+    if (R >= (int)p.M || col >= (int)p.N) continue;
+    if (p.out_bf16 && gridDim.y == 1) {
+      u32x2 o;
+      o.x = pack_bf16x2(s4.x, s4.y);
+      o.y = pack_bf16x2(s4.z, s4.w);
+      *(u32x2*)((uint16_t*)p.y + (size_t)R * p.N + col) = o;
+    } else {
+      // f32 output or partial plane; Y is only guaranteed 8-byte aligned.
+      float* yp = (float*)((char*)p.y + (gridDim.y > 1 ? (size_t)blockIdx.y * p.y_split_stride : 0));
+      f32x2_t* o = (f32x2_t*)(yp + (size_t)R * p.N + col);
+      o[0] = f32x2_t{s4.x, s4.y};
+      o[1] = f32x2_t{s4.z, s4.w};
+    }
+  }
+}
+
+}  // namespace t0mi
