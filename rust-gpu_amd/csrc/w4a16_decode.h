@@ -102,7 +102,6 @@ __global__ __launch_bounds__(NW * 64) void w4a16_decode_v2(W4Params p) {
   const int kb0 = __builtin_amdgcn_readfirstlane(((int)blockIdx.y * NW + wave) * KBW);
   int nkb = kb_tot - kb0;  // valid k-blocks of this wave (wave-uniform)
   nkb = nkb < 0 ? 0 : (nkb > KBW ? KBW : nkb);
-  const int arow = c < (int)p.M ? c : 0;
 
   const int ngroups = kb_tot / KBPG;
   const uint32_t mask = p.nib_mask, magic = p.nib_magic;
@@ -111,21 +110,51 @@ __global__ __launch_bounds__(NW * 64) void w4a16_decode_v2(W4Params p) {
 #pragma unroll
   for (int j = 0; j < 4; ++j) acc[j] = (f32x4){0.f, 0.f, 0.f, 0.f};
 
+  // Activation slices are loaded 1 KB (8 rows x one 128-byte line of 64 K
+  // values) per instruction, stored to LDS and read back in the MFMA layout
+  // with ds_read_b128.  Piece (row 8h + r, 16-byte chunk x) of the block
+  // (pair p, half h) sits in slot
+  //   slot(h, r, x) = 16 * (x >> 1) + ((8h + r) ^ (8 * (x & 1) + (x >> 1))),
+  // so for a fixed chunk the 16 rows fall in 16 distinct 16-byte bank groups
+  // and the fragment reads (16 rows x one chunk per 16 lanes) are free of bank
+  // conflicts.
+  static_assert(KBW % 2 == 0, "k-blocks are moved in pairs");
+  constexpr int SMEM_KB = KBW > 4 ? KBW : 4;  // per wave: activations, then the reduction
+  __shared__ __attribute__((aligned(1024))) float smem[NW * SMEM_KB * 256];
+  const uint32_t lds_wave = lds_addr(smem) + (uint32_t)(wave * KBW * 1024);
+  // Loads: the 16 lanes of quarter k read rows k and k+4 (two whole lines) of
+  // the 8-row half; the two rows' slot sets are disjoint, so the stores are
+  // conflict-free too.
+  const int ld_r = (lane >> 4) + 4 * ((lane >> 3) & 1), ld_x = lane & 7;
+  auto slot = [](int h, int r, int x) { return 16 * (x >> 1) + ((8 * h + r) ^ (8 * (x & 1) + (x >> 1))); };
+  const int st_off[2] = {16 * slot(0, ld_r, ld_x), 1024 + 16 * slot(1, ld_r, ld_x)};
+  int rd_off[2];  // fragment byte offset for k-block parity 0 / 1
+#pragma unroll
+  for (int beta = 0; beta < 2; ++beta) {
+    const int h = c >> 3, r = c & 7, x = 4 * beta + g;
+    rd_off[beta] = h * 1024 + 16 * slot(h, r, x);
+  }
+
   // FULL: all KBW blocks of the wave exist (every wave but those at the ragged
   // end of K); then nothing is clamped or skipped and no branch separates the
   // loads from their uses.
   auto body = [&](auto full_c) {
     constexpr bool FULL = decltype(full_c)::value;
-    u32x4 wv[KBW], av[KBW];
+    u32x4 wv[KBW], at[KBW];
     u32x2 sv[NG];
     uint32_t zv[NG];
-    // Activations (L2-resident) and scales first, weights last: loads complete
-    // in issue order, so block b's dequant waits only for weight row b.
+    // Activation loads (L2-resident) first, then scales, weights last: loads
+    // complete in issue order, so block b's dequant waits only for weight row b.
 #pragma unroll
-    for (int b = 0; b < KBW; ++b) {
-      int kb = kb0 + b;
-      if (!FULL) kb = kb < kb_tot ? kb : kb_tot - 1;
-      av[b] = *(const u32x4*)(p.a + (size_t)arow * p.K + kb * 32 + g * 8);
+    for (int pp = 0; pp < KBW / 2; ++pp) {
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        int row = 8 * h + ld_r;
+        row = row < (int)p.M ? row : 0;
+        int kofs = (kb0 + 2 * pp) * 32 + 8 * ld_x;
+        if (!FULL) kofs = kofs + 8 <= (int)p.K ? kofs : 0;
+        at[2 * pp + h] = *(const u32x4*)(p.a + (size_t)row * p.K + kofs);
+      }
     }
 #pragma unroll
     for (int q = 0; q < NG; ++q) {
@@ -142,6 +171,11 @@ __global__ __launch_bounds__(NW * 64) void w4a16_decode_v2(W4Params p) {
     }
     // Every load is issued before the first dequant: nothing may move across.
     __builtin_amdgcn_sched_barrier(0);
+    // Activation pieces -> this wave's LDS slice (slot = lane), read back below
+    // in the MFMA layout; LDS operations of one wave complete in order.
+#pragma unroll
+    for (int i = 0; i < KBW; ++i)
+      *(__attribute__((address_space(3))) u32x4*)(size_t)(lds_wave + (uint32_t)((i >> 1) * 2048 + st_off[i & 1])) = at[i];
 #pragma unroll
     for (int q = 0; q < NG; ++q) {
       if (!FULL && q * KBPG >= nkb) break;  // wave-uniform: the ragged end of K
@@ -151,7 +185,9 @@ __global__ __launch_bounds__(NW * 64) void w4a16_decode_v2(W4Params p) {
 #pragma unroll
       for (int i = 0; i < KBPG; ++i) {
         const int b = q * KBPG + i;
-        const bf16x8_t A = perm_act(av[b]);
+        const u32x4 av = *(const __attribute__((address_space(3))) u32x4*)(size_t)(
+            lds_wave + (uint32_t)((b >> 1) * 2048 + rd_off[b & 1]));
+        const bf16x8_t A = perm_act(av);
         S = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A, ones, S, 0, 0, 0);
         P[0] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A, nib_pairs_ao(wv[b].x, mask, magic), P[0], 0, 0, 0);
         P[1] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A, nib_pairs_ao(wv[b].y, mask, magic), P[1], 0, 0, 0);
@@ -179,7 +215,8 @@ __global__ __launch_bounds__(NW * 64) void w4a16_decode_v2(W4Params p) {
   // Lane (c, g) holds rows 4g + r, columns 4c + j as acc[j][r].  Stage them as
   // red[wave][row][col] so that each of 256 threads sums one row segment of
   // 4 columns over the waves (in wave order) and stores it with one vector store.
-  __shared__ __attribute__((aligned(16))) float red[NW * 16 * 64];
+  __syncthreads();  // every wave is done with its activation slice
+  float* red = smem;
   float* mine = red + wave * 16 * 64;
 #pragma unroll
   for (int r = 0; r < 4; ++r)
