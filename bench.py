@@ -31,7 +31,7 @@ METRIC = "bf16 GEMM TFLOPS @4096³ (% MFMA peak); W4A16 decode HBM GB/s (% peak)
 def parse():
     p = argparse.ArgumentParser()
     p.add_argument("--gpus", type=int, default=1)
-    p.add_argument("--steps", type=int, default=50)
+    p.add_argument("--steps", type=int, default=200)
     p.add_argument("--warmup", type=int, default=10)
     p.add_argument("--only", choices=["all", "gemm", "w4a16", "copy"], default="all",
                    help="'copy' runs only a plain 1 GiB fp32 copy kernel: the calibration for rocprofv3 "
@@ -52,6 +52,20 @@ def load_traffic(kernel_key):
         return None
 
 
+def warm_up(torch, launch, n: int, min_s: float = 0.3):
+    """n untimed launches, then more until min_s seconds of back-to-back work have run:
+    the clock and power state settle within a few hundred milliseconds of sustained load,
+    and the timed region should see that steady state, not the first milliseconds."""
+    for _ in range(n):
+        launch()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    while time.perf_counter() - t0 < min_s:
+        for _ in range(20):
+            launch()
+        torch.cuda.synchronize()
+
+
 def bench_gemm(args, torch, t0mi, rt):
     M = N = K = 4096
     g = torch.Generator(device="cuda:0")
@@ -62,12 +76,10 @@ def bench_gemm(args, torch, t0mi, rt):
     if args.config:
         cfg = t0mi.preset(args.config)
     else:
-        cfg = t0mi.auto_select(M, K, N)
+        cfg = t0mi.auto_select_layout(M, K, N, t0mi.NN, t0mi.OUT_BF16)
     cfg = cfg.copy(transpose=t0mi.NN, out_dtype=t0mi.OUT_BF16)
     pa, pb, py = a.data_ptr(), b.data_ptr(), y.data_ptr()
-    for _ in range(args.warmup):
-        rt.gemm(cfg, pa, pb, py, M, N, K)
-    torch.cuda.synchronize()
+    warm_up(torch, lambda: rt.gemm(cfg, pa, pb, py, M, N, K), args.warmup)
     e0 = torch.cuda.Event(enable_timing=True)
     e1 = torch.cuda.Event(enable_timing=True)
     t_host0 = time.perf_counter()
@@ -99,10 +111,14 @@ def bench_w4a16(args, torch, t0mi, rt):
           for _ in range(copies)]
     y = torch.empty(Mw, Nw, device="cuda:0", dtype=torch.bfloat16)
     calls = max(args.steps * 4, 2 * copies)
-    for i in range(max(args.warmup, copies)):
-        rt.w4a16_gemm(a.data_ptr(), ws[i % copies].data_ptr(), ss[i % copies].data_ptr(), 0, 8, y.data_ptr(),
-                      Mw, Kw, Nw, G, t0mi.OUT_BF16)
-    torch.cuda.synchronize()
+    rot = [0]
+
+    def launch():
+        j = rot[0] % copies
+        rot[0] += 1
+        rt.w4a16_gemm(a.data_ptr(), ws[j].data_ptr(), ss[j].data_ptr(), 0, 8, y.data_ptr(), Mw, Kw, Nw, G,
+                      t0mi.OUT_BF16)
+    warm_up(torch, launch, max(args.warmup, copies))
     e0 = torch.cuda.Event(enable_timing=True)
     e1 = torch.cuda.Event(enable_timing=True)
     e0.record()

@@ -124,6 +124,11 @@ int t0mi_build_kernargs_with_bias(uint64_t x, uint64_t wt, uint64_t y, uint32_t 
 int t0mi_auto_select(uint32_t m, uint32_t k, uint32_t n, t0mi_gemm_config* out);
 /* auto_select_legacy (gemm_gen.rs:351-404), re-derived for gfx950. */
 int t0mi_auto_select_legacy(uint32_t m, uint32_t k, uint32_t n, t0mi_gemm_config* out);
+/* gfx950 extension of auto_select (gemm_gen.rs:340), which only knows the NT
+ * layout and f32 output: the same ranking for a given layout (t0mi_transpose)
+ * and out_dtype, over the kernels prebuilt for that layout. */
+int t0mi_auto_select_layout(uint32_t m, uint32_t k, uint32_t n, uint32_t transpose, uint32_t out_dtype,
+                            t0mi_gemm_config* out);
 /* cached_auto_select (src/t0/prefill_spec_cache.rs:42-76): process-wide cache. */
 int t0mi_cached_auto_select(uint32_t m, uint32_t k, uint32_t n, t0mi_gemm_config* out);
 void t0mi_clear_spec_cache(void);
@@ -338,6 +343,67 @@ int t0mi_w4a16_gemm(t0mi_ctx* ctx, uint64_t a, uint64_t qweight, uint64_t scales
  * quant_kernels.rs:167-168); 2: bf16 round-to-nearest-even.  Bit-exact. */
 int t0mi_dequant_int4(t0mi_ctx* ctx, uint64_t qweight, uint64_t scales, uint64_t qzeros, uint32_t zp_const,
                       uint64_t out, uint32_t k, uint32_t n, uint32_t group, uint32_t round_mode);
+
+/* ---- GPTQ container (GptqWeight, src/t0/quant_kernels.rs:177-294) ---------- */
+/* Byte layout of GptqWeight::from_bytes (quant_kernels.rs:242-286), little-endian:
+ *   [rows u32][cols u32][group_size u32][rows*cols/2 packed INT4 bytes, element
+ *   2i = low nibble of byte i, row-major [rows][cols]][n_groups*rows f32 scales]
+ *   [n_groups*rows i32 zero points], scale/zero of (row, g) at row*n_groups + g,
+ *   n_groups = cols / group_size.  rows = output features (N), cols = K. */
+typedef struct t0mi_gptq_info {
+  uint32_t rows, cols, group_size, n_groups;
+  uint64_t packed_offset, packed_bytes;  /* 12, rows*cols/2 */
+  uint64_t scales_offset, zeros_offset;  /* f32 and i32 sections */
+  uint64_t total_bytes;                  /* 12 + packed + 8 * n_groups * rows */
+  uint32_t zeros_in_range;               /* 1: every zero point is 0..15 (packable to INT4) */
+  uint32_t scales_bf16_exact;            /* 1: every scale is exactly a bf16 value */
+} t0mi_gptq_info;
+
+/* GptqWeight::from_bytes (quant_kernels.rs:242-286): validates the header and
+ * section lengths of `raw` and fills `out`.  The reference panics on a short
+ * header, a truncated body or a length mismatch; here those return
+ * T0MI_ERR_INVALID (as does group_size 0 or an odd rows*cols).  Host only. */
+int t0mi_gptq_parse(const void* raw, size_t len, t0mi_gptq_info* out);
+/* GptqWeight::gpu_buffer_size (quant_kernels.rs:289-293): packed + 4*scales + 4*zeros bytes. */
+uint64_t t0mi_gptq_gpu_buffer_size(const t0mi_gptq_info* info);
+
+/* New: converts the GPTQ sections, already in device memory, to the W4A16
+ * layouts of t0mi_w4a16_gemm (K = cols, N = rows), on ctx's stream:
+ *   qweight u32 [K/8][N]  <- packed [N][K/2] bytes (a u32 transpose: the GPTQ
+ *                            bytes of one row, read as little-endian words, are
+ *                            the W4A16 words);
+ *   scales  bf16 [K/g][N] <- f32 [N][K/g], rounded to nearest even (exact when
+ *                            t0mi_gptq_info.scales_bf16_exact);
+ *   qzeros  u32 [K/g][N/8] <- i32 [N][K/g] packed as nibbles (values must be
+ *                            0..15: t0mi_gptq_info.zeros_in_range).
+ * Requires K % 8 == 0, N % 8 == 0, K % group == 0.  Asynchronous. */
+int t0mi_gptq_convert(t0mi_ctx* ctx, uint64_t packed, uint64_t scales_f32, uint64_t zeros_i32, uint32_t rows,
+                      uint32_t cols, uint32_t group, uint64_t qweight, uint64_t scales_bf16, uint64_t qzeros);
+
+/* ---- Ignis matmul caller (src/ignis/ops/bf16_matmul.rs:33-423) ------------- */
+/* The reference converts f32 -> bf16 on the host (round to nearest even,
+ * bf16_matmul.rs:372), transposes W, pads every dimension to tile multiples,
+ * runs the NT gemm_gen kernel with f32 output and unpads.  Here the conversion
+ * (and, where a GEMM operand needs it, the transpose) runs on the GPU into a
+ * library-owned buffer, NN is native and ragged shapes need no padding.  All
+ * buffers are device f32, row-major, and the calls are asynchronous. */
+
+/* f32 -> bf16 round-to-nearest-even of `count` elements (bf16_matmul.rs:372). */
+int t0mi_f32_to_bf16(t0mi_ctx* ctx, uint64_t src_f32, uint64_t dst_bf16, uint64_t count);
+/* matmul forward (bf16_matmul.rs:33-96, dispatch_gemm_forward :159-209):
+ * Y[m,n] = bf16(X[m,k]) . bf16(W[k,n]), fp32 accumulate, f32 out. */
+int t0mi_matmul_f32(t0mi_ctx* ctx, uint64_t x, uint64_t w, uint64_t y, uint32_t m, uint32_t k, uint32_t n);
+/* matmul_with_wt_bf16 (bf16_matmul.rs:99-134): X f32 [m,k], WT bf16 [n,k]
+ * (pre-transposed weight) -> Y f32 [m,n].  Requires k % 8 == 0 and n % 8 == 0
+ * (WT is used in place). */
+int t0mi_matmul_wt_bf16(t0mi_ctx* ctx, uint64_t x, uint64_t wt_bf16, uint64_t y, uint32_t m, uint32_t k,
+                        uint32_t n);
+/* gemm_backward_data (bf16_matmul.rs:216-262): dX[m,k] = bf16(dY[m,n]) . bf16(W[k,n])^T. */
+int t0mi_matmul_backward_data(t0mi_ctx* ctx, uint64_t dy, uint64_t w, uint64_t dx, uint32_t m, uint32_t k,
+                              uint32_t n);
+/* gemm_backward_weight (bf16_matmul.rs:268-316): dW[k,n] = bf16(X[m,k])^T . bf16(dY[m,n]). */
+int t0mi_matmul_backward_weight(t0mi_ctx* ctx, uint64_t x, uint64_t dy, uint64_t dw, uint32_t m, uint32_t k,
+                                uint32_t n);
 
 #ifdef __cplusplus
 }

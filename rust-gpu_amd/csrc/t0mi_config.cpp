@@ -443,6 +443,19 @@ extern "C" int t0mi_auto_select(uint32_t m, uint32_t k, uint32_t n, t0mi_gemm_co
   return T0MI_OK;
 }
 
+extern "C" int t0mi_auto_select_layout(uint32_t m, uint32_t k, uint32_t n, uint32_t transpose, uint32_t out_dtype,
+                                       t0mi_gemm_config* out) {
+  // auto_select for a given B layout and output type: the same cost-model
+  // ranking, restricted to prebuilt kernels of that layout (NN needs tile_n >= 64).
+  if (!out) return set_error(T0MI_ERR_INVALID, "null config");
+  if (!m || !n || !k) return set_error(T0MI_ERR_INVALID, "zero dimension");
+  if (transpose > T0MI_NN || out_dtype > T0MI_OUT_BF16) return set_error(T0MI_ERR_INVALID, "bad layout or out_dtype");
+  auto c = rank_candidates(m, n, k, transpose, out_dtype, nullptr);
+  if (c.empty()) return set_error(T0MI_ERR_NO_KERNEL, "no prebuilt kernel for %ux%ux%u", m, n, k);
+  *out = c[0];
+  return T0MI_OK;
+}
+
 extern "C" int t0mi_auto_select_legacy(uint32_t m, uint32_t k, uint32_t n, t0mi_gemm_config* out) {
   // The shape buckets of auto_select_legacy (src/t0/gemm_gen.rs:351-404), with
   // gfx950 tiles: large squares take the 256x256 8-wave tile, thin/small

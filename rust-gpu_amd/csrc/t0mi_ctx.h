@@ -56,6 +56,10 @@ struct t0mi_ctx {
   // Library-owned workspace (split-K partial planes, W4A16 partials).
   void* ws = nullptr;
   size_t ws_bytes = 0;
+  // Library-owned bf16 operand buffer of the Ignis matmul calls (kept apart
+  // from ws, which the GEMMs they launch may use for split-K).
+  void* cvt = nullptr;
+  size_t cvt_bytes = 0;
   // Null backend: injected failure and the last recorded dispatch.
   bool inject_timeout = false;
   uint32_t last_grid[3] = {0, 0, 0};
@@ -66,6 +70,12 @@ struct t0mi_ctx {
 namespace t0mi {
 // Grows ctx->ws to at least `bytes` (waits for the stream first).
 int ensure_workspace(t0mi_ctx* ctx, size_t bytes);
+// Grows ctx->cvt to at least `bytes` (waits for the stream first).
+int ensure_cvt_buffer(t0mi_ctx* ctx, size_t bytes);
+// Runs a GEMM with the best prebuilt config for (m, n, k, transpose) and f32
+// output (cost-model ranking, as t0mi_auto_select).  Asynchronous.
+int run_gemm_auto(t0mi_ctx* ctx, uint32_t transpose, uint64_t x, uint64_t b, uint64_t y, uint32_t m, uint32_t n,
+                  uint32_t k);
 // Launches the bf16 GEMM kernel for (cfg, params) on ctx's stream.
 int launch_gemm(t0mi_ctx* ctx, const t0mi_gemm_config& cfg, const GemmLaunchEntry* e, GemmParams p);
 int check_ctx(t0mi_ctx* ctx);

@@ -68,6 +68,24 @@ int ensure_workspace(t0mi_ctx* ctx, size_t bytes) {
   return T0MI_OK;
 }
 
+int ensure_cvt_buffer(t0mi_ctx* ctx, size_t bytes) {
+  if (ctx->cvt_bytes >= bytes) return T0MI_OK;
+  if (ctx->null_backend) {
+    ctx->cvt_bytes = bytes;
+    return T0MI_OK;
+  }
+  hipError_t e = hipStreamSynchronize(ctx->stream);
+  if (e != hipSuccess) return hip_fail(e, "hipStreamSynchronize");
+  if (ctx->cvt) (void)hipFree(ctx->cvt);
+  ctx->cvt = nullptr;
+  ctx->cvt_bytes = 0;
+  size_t want = bytes + (bytes >> 2);
+  e = hipMalloc(&ctx->cvt, want);
+  if (e != hipSuccess) return hip_fail(e, "hipMalloc(conversion buffer)");
+  ctx->cvt_bytes = want;
+  return T0MI_OK;
+}
+
 int launch_gemm(t0mi_ctx* ctx, const t0mi_gemm_config& cfg, const GemmLaunchEntry* e, GemmParams p) {
   const uint32_t nwg = p.tiles_m * p.tiles_n * p.split_k;
   if (nwg == 0) return T0MI_OK;
@@ -223,6 +241,7 @@ extern "C" void t0mi_ctx_destroy(t0mi_ctx* ctx) {
     if (!ctx->poisoned.load()) (void)hipStreamSynchronize(ctx->stream);
     for (auto& kv : ctx->allocs) (void)hipFree((void*)kv.first);
     if (ctx->ws) (void)hipFree(ctx->ws);
+    if (ctx->cvt) (void)hipFree(ctx->cvt);
     if (ctx->own_stream) (void)hipStreamDestroy(ctx->stream);
   }
   delete ctx;
@@ -608,6 +627,17 @@ extern "C" int t0mi_gemm(t0mi_ctx* ctx, const t0mi_gemm_config* cfg, uint64_t x,
   const GemmLaunchEntry* e = find_gemm_launch(*cfg);
   if (!e) return set_error(T0MI_ERR_NO_KERNEL, "[t0mi] no prebuilt gfx950 kernel for '%s'", config_name(*cfg).c_str());
   return run_gemm(ctx, *cfg, e, x, b, y, bias, m, n, k, chain_of(cfg->epilogue));
+}
+
+int t0mi::run_gemm_auto(t0mi_ctx* ctx, uint32_t transpose, uint64_t x, uint64_t b, uint64_t y, uint32_t m, uint32_t n,
+                  uint32_t k) {
+  const std::vector<t0mi_gemm_config> cands = rank_candidates(m, n, k, transpose, T0MI_OUT_F32, nullptr);
+  for (const t0mi_gemm_config& c : cands) {
+    const GemmLaunchEntry* e = find_gemm_launch(c);
+    if (e) return run_gemm(ctx, c, e, x, b, y, 0, m, n, k, EpiChain{});
+  }
+  return set_error(T0MI_ERR_NO_KERNEL, "[t0mi] no prebuilt gfx950 kernel for %ux%ux%u (%s)", m, n, k,
+                   transpose == T0MI_NN ? "NN" : "NT");
 }
 
 // ------------------------------------------------------------ tile_ir GEMM ----

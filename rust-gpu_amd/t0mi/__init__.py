@@ -158,6 +158,7 @@ SIGNATURES = {
     "t0mi_build_kernargs_with_bias": (_I, [_U64, _U64, _U64, _U32, _U32, _U32, _CFG, _U64, _P]),
     "t0mi_auto_select": (_I, [_U32, _U32, _U32, _CFG]),
     "t0mi_auto_select_legacy": (_I, [_U32, _U32, _U32, _CFG]),
+    "t0mi_auto_select_layout": (_I, [_U32, _U32, _U32, _U32, _U32, _CFG]),
     "t0mi_cached_auto_select": (_I, [_U32, _U32, _U32, _CFG]),
     "t0mi_clear_spec_cache": (None, []),
     "t0mi_spec_cache_len": (_SZ, []),
@@ -212,6 +213,14 @@ SIGNATURES = {
     "t0mi_tile_gemm": (_I, [_P, _TS, _U64, _U64, _U64, _U32, _U32, _U32, _U64, _F32, _F32, _F32]),
     "t0mi_w4a16_gemm": (_I, [_P, _U64, _U64, _U64, _U64, _U32, _U64, _U32, _U32, _U32, _U32, _U32]),
     "t0mi_dequant_int4": (_I, [_P, _U64, _U64, _U64, _U32, _U64, _U32, _U32, _U32, _U32]),
+    "t0mi_gptq_parse": (_I, [_P, _SZ, _P]),
+    "t0mi_gptq_gpu_buffer_size": (_U64, [_P]),
+    "t0mi_gptq_convert": (_I, [_P, _U64, _U64, _U64, _U32, _U32, _U32, _U64, _U64, _U64]),
+    "t0mi_f32_to_bf16": (_I, [_P, _U64, _U64, _U64]),
+    "t0mi_matmul_f32": (_I, [_P, _U64, _U64, _U64, _U32, _U32, _U32]),
+    "t0mi_matmul_wt_bf16": (_I, [_P, _U64, _U64, _U64, _U32, _U32, _U32]),
+    "t0mi_matmul_backward_data": (_I, [_P, _U64, _U64, _U64, _U32, _U32, _U32]),
+    "t0mi_matmul_backward_weight": (_I, [_P, _U64, _U64, _U64, _U32, _U32, _U32]),
 }
 
 
@@ -329,6 +338,13 @@ def auto_select(m: int, k: int, n: int) -> GemmConfig:
     """``gemm_gen::auto_select(m, k, n)`` — note the (m, k, n) order."""
     c = GemmConfig()
     check(lib().t0mi_auto_select(m, k, n, ctypes.byref(c)))
+    return c
+
+
+def auto_select_layout(m: int, k: int, n: int, transpose: int = NN, out_dtype: int = OUT_F32) -> GemmConfig:
+    """auto_select for a given B layout and output dtype (gfx950 extension of gemm_gen.rs:340)."""
+    c = GemmConfig()
+    check(lib().t0mi_auto_select_layout(m, k, n, transpose, out_dtype, ctypes.byref(c)))
     return c
 
 
@@ -535,10 +551,84 @@ class Runtime:
                      k: int, n: int, group: int, round_mode: int) -> None:
         check(lib().t0mi_dequant_int4(self.handle, qweight, scales, qzeros, zp_const, out, k, n, group, round_mode))
 
+    # ---- Ignis matmul caller (src/ignis/ops/bf16_matmul.rs:33-423) ----
+    def f32_to_bf16(self, src: int, dst: int, count: int) -> None:
+        """f32 -> bf16 round-to-nearest-even on the GPU (bf16_matmul.rs:372)."""
+        check(lib().t0mi_f32_to_bf16(self.handle, src, dst, count))
+
+    def matmul(self, x: int, w: int, y: int, m: int, k: int, n: int) -> None:
+        """``matmul`` forward (bf16_matmul.rs:33-96): Y[m,n] = bf16(X) . bf16(W), f32 in and out."""
+        check(lib().t0mi_matmul_f32(self.handle, x, w, y, m, k, n))
+
+    def matmul_with_wt_bf16(self, x: int, wt_bf16: int, y: int, m: int, k: int, n: int) -> None:
+        """``matmul_with_wt_bf16`` (bf16_matmul.rs:99-134): X f32 [m,k], WT bf16 [n,k]."""
+        check(lib().t0mi_matmul_wt_bf16(self.handle, x, wt_bf16, y, m, k, n))
+
+    def matmul_backward_data(self, dy: int, w: int, dx: int, m: int, k: int, n: int) -> None:
+        """``gemm_backward_data`` (bf16_matmul.rs:216-262): dX = dY . W^T."""
+        check(lib().t0mi_matmul_backward_data(self.handle, dy, w, dx, m, k, n))
+
+    def matmul_backward_weight(self, x: int, dy: int, dw: int, m: int, k: int, n: int) -> None:
+        """``gemm_backward_weight`` (bf16_matmul.rs:268-316): dW = X^T . dY."""
+        check(lib().t0mi_matmul_backward_weight(self.handle, x, dy, dw, m, k, n))
+
+    def gptq_convert(self, packed: int, scales_f32: int, zeros_i32: int, rows: int, cols: int, group: int,
+                     qweight: int, scales_bf16: int, qzeros: int) -> None:
+        """GPTQ sections (device) -> t0mi_w4a16_gemm layouts (K = cols, N = rows)."""
+        check(lib().t0mi_gptq_convert(self.handle, packed, scales_f32, zeros_i32, rows, cols, group, qweight,
+                                      scales_bf16, qzeros))
+
     def auto_gemm(self, a: int, b: int, c: int, m: int, n: int, k: int) -> float:
         tf = ctypes.c_double()
         check(lib().t0mi_auto_gemm(self.handle, a, b, c, m, n, k, ctypes.byref(tf)))
         return tf.value
+
+
+class GptqInfo(ctypes.Structure):
+    """``t0mi_gptq_info``: the header and section offsets of a GPTQ byte container."""
+    _fields_ = [("rows", ctypes.c_uint32), ("cols", ctypes.c_uint32), ("group_size", ctypes.c_uint32),
+                ("n_groups", ctypes.c_uint32), ("packed_offset", ctypes.c_uint64), ("packed_bytes", ctypes.c_uint64),
+                ("scales_offset", ctypes.c_uint64), ("zeros_offset", ctypes.c_uint64),
+                ("total_bytes", ctypes.c_uint64), ("zeros_in_range", ctypes.c_uint32),
+                ("scales_bf16_exact", ctypes.c_uint32)]
+
+
+class GptqWeight:
+    """``GptqWeight`` (src/t0/quant_kernels.rs:188-294): rows = output features (N),
+    cols = input features (K); packed INT4 bytes [rows][cols/2] (element 2i = low
+    nibble of byte i), f32 scales and i32 zero points at [row * n_groups + g]."""
+
+    def __init__(self, raw: bytes, info: GptqInfo):
+        self.raw = raw
+        self.info = info
+        self.rows, self.cols, self.group_size, self.n_groups = info.rows, info.cols, info.group_size, info.n_groups
+
+    @classmethod
+    def from_bytes(cls, raw: bytes) -> "GptqWeight":
+        """``GptqWeight::from_bytes`` (quant_kernels.rs:242-286); raises T0miError where the reference panics."""
+        info = GptqInfo()
+        buf = ctypes.create_string_buffer(bytes(raw), len(raw)) if len(raw) else ctypes.create_string_buffer(1)
+        check(lib().t0mi_gptq_parse(buf, len(raw), ctypes.byref(info)))
+        return cls(bytes(raw), info)
+
+    def gpu_buffer_size(self) -> int:
+        """``GptqWeight::gpu_buffer_size`` (quant_kernels.rs:289-293)."""
+        return int(lib().t0mi_gptq_gpu_buffer_size(ctypes.byref(self.info)))
+
+    @property
+    def packed_weights(self) -> bytes:
+        i = self.info
+        return self.raw[i.packed_offset:i.packed_offset + i.packed_bytes]
+
+    @property
+    def scales_bytes(self) -> bytes:
+        i = self.info
+        return self.raw[i.scales_offset:i.zeros_offset]
+
+    @property
+    def zeros_bytes(self) -> bytes:
+        i = self.info
+        return self.raw[i.zeros_offset:i.total_bytes]
 
 
 class GemmTuner:
