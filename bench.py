@@ -33,9 +33,10 @@ def parse():
     p.add_argument("--gpus", type=int, default=1)
     p.add_argument("--steps", type=int, default=200)
     p.add_argument("--warmup", type=int, default=10)
-    p.add_argument("--only", choices=["all", "gemm", "w4a16", "copy"], default="all",
+    p.add_argument("--only", choices=["all", "gemm", "w4a16", "copy", "dispatch"], default="all",
                    help="'copy' runs only a plain 1 GiB fp32 copy kernel: the calibration for rocprofv3 "
-                        "FETCH_SIZE/WRITE_SIZE readings")
+                        "FETCH_SIZE/WRITE_SIZE readings; 'dispatch' times batched submission (a batch of "
+                        "small GEMM dispatches: synchronous, DispatchQueue, HIP graph)")
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     p.add_argument("--config", default=None, help="GEMM preset name to force (default: auto_select)")
     return p.parse_args()
@@ -199,6 +200,79 @@ def copy_calibration(args, torch):
                       "ms_per_launch": round(ms, 4), "GB/s": round(nbytes / (ms * 1e-3) / 1e9, 1)}), flush=True)
 
 
+def bench_dispatch(args, torch, t0mi):
+    """Host-visible cost per dispatch of a batch of small GEMMs (the prefill_dispatch.rs
+    scenario: dozens of layers x a few kernels), three ways: a synchronous dispatch per
+    kernel (GpuRuntime::dispatch), one DispatchQueue flush per batch, and one replay of
+    the batch captured as a HIP graph.  Wall time from the first submit to the end of
+    the final wait, median over repeats; the kernels are the same in all three."""
+    batch, reps = 128, max(5, min(args.steps, 50))
+    cfg = t0mi.preset("tile_64x64_k32")
+    m = n = 128
+    k = 256
+    rt = t0mi.Runtime(device=0)  # own stream: a graph cannot be captured on the null stream
+    kern = rt.kernel(cfg)
+    g = torch.Generator(device="cuda:0")
+    g.manual_seed(0x7601)
+    a = torch.randn(m, k, device="cuda:0", generator=g).to(torch.bfloat16)
+    bs = [torch.randn(n, k, device="cuda:0", generator=g).to(torch.bfloat16) for _ in range(8)]
+    ys = [torch.empty(m, n, device="cuda:0", dtype=torch.float32) for _ in range(batch)]
+    torch.cuda.synchronize()
+    grid = t0mi.compute_grid_auto(cfg, m, n)
+    kas = [t0mi.build_kernargs(a.data_ptr(), bs[i % 8].data_ptr(), ys[i].data_ptr(), k, n, m, cfg)
+           for i in range(batch)]
+
+    def sync_each():
+        for ka in kas:
+            t0mi.check(rt.dispatch(kern, grid, ka, sync=True))
+
+    def queued():
+        dq = t0mi.DispatchQueue(rt)
+        for ka in kas:
+            dq.submit(kern, grid, ka)
+        assert dq.flush() == batch
+
+    rt.capture_begin()
+    for ka in kas:
+        t0mi.check(rt.dispatch(kern, grid, ka, sync=False))
+    graph = rt.capture_end()
+
+    def replay():
+        graph.launch()
+        t0mi.check(rt.wait_idle())
+
+    # GPU time of one replay (kernels plus the gaps between them), from events
+    # recorded on the runtime's own stream.
+    ext = torch.cuda.ExternalStream(rt.stream)
+    replay()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(ext)
+    graph.launch()
+    e1.record(ext)
+    t0mi.check(rt.wait_idle())
+    e1.synchronize()
+    gpu_us = e0.elapsed_time(e1) * 1e3 / batch
+
+    res = {}
+    for name, fn in (("sync", sync_each), ("queue", queued), ("graph", replay)):
+        for _ in range(3):
+            fn()
+        ts = []
+        for _ in range(reps):
+            t0 = time.perf_counter()
+            fn()
+            ts.append(time.perf_counter() - t0)
+        ts.sort()
+        res[name] = round(ts[len(ts) // 2] / batch * 1e6, 3)
+    graph.destroy()
+    rt.close()
+    print(json.dumps({"metric": "host-visible time per dispatch in a batch (us)", "unit": "us/dispatch",
+                      "higher_is_better": False, "batch": batch, "repeats": reps, "per_dispatch_us": res,
+                      "gpu_us_per_dispatch_in_graph": round(gpu_us, 3),
+                      "config": {"workload": f"{batch} dispatches of a {m}x{n}x{k} NT bf16 GEMM, f32 out",
+                                 "kernel": cfg.name()}}), flush=True)
+
+
 def main():
     args = parse()
     if args.gpus != 1:
@@ -211,6 +285,9 @@ def main():
         copy_calibration(args, torch)
         return
     import t0mi
+    if args.only == "dispatch":
+        bench_dispatch(args, torch, t0mi)
+        return
     rt = t0mi.Runtime.on_torch_stream(0)
     out = {"metric": METRIC, "n_gpus": 1, "steps": args.steps, "warmup": args.warmup, "higher_is_better": True,
            "scaling": "weak", "vs_baseline": None, "dtype": "bf16", "data": "synthetic"}

@@ -43,6 +43,7 @@ extern "C" {
 #define T0MI_ERR_TIMEOUT (-6)   /* dispatch did not complete in time; runtime poisoned */
 #define T0MI_ERR_NOT_FOUND (-7) /* cache miss / unknown preset */
 #define T0MI_ERR_NO_DEVICE (-8) /* no gfx950 device visible */
+#define T0MI_ERR_CAPTURE (-9)   /* call cannot run while the runtime's stream is captured */
 
 /* Thread-local description of the last error on this thread. */
 const char* t0mi_last_error(void);
@@ -196,6 +197,47 @@ int t0mi_wait_idle(t0mi_ctx* ctx);
  * (p = 0..split_k-1 order) using a library-owned workspace.  Asynchronous. */
 int t0mi_gemm(t0mi_ctx* ctx, const t0mi_gemm_config* cfg, uint64_t x, uint64_t b, uint64_t y,
               uint64_t bias, uint32_t m, uint32_t n, uint32_t k);
+
+/* ---- batched submission: DispatchQueue (src/t0/prefill_dispatch.rs:58-214) - */
+typedef struct t0mi_dispatch_queue t0mi_dispatch_queue;
+/* DispatchQueue::new (prefill_dispatch.rs:73-79). */
+int t0mi_dq_new(t0mi_ctx* ctx, t0mi_dispatch_queue** out);
+/* DispatchQueue::submit (prefill_dispatch.rs:90-107): dispatch_async with the
+ * same checks as t0mi_dispatch (kernarg length, grid); a poisoned runtime
+ * refuses with T0MI_ERR_POISONED "[DispatchQueue] Queue poisoned ...". */
+int t0mi_dq_submit(t0mi_dispatch_queue* q, const t0mi_kernel* k, const uint32_t grid_workitems[3],
+                   const uint8_t* ka, size_t ka_len);
+/* DispatchQueue::flush (prefill_dispatch.rs:133-166): one wait for every
+ * pending dispatch (timeout / failure poisons the runtime); *count = the
+ * number flushed (0 when none were pending, without waiting). */
+int t0mi_dq_flush(t0mi_dispatch_queue* q, size_t* count);
+/* DispatchQueue::pending (prefill_dispatch.rs:169-171). */
+size_t t0mi_dq_pending(const t0mi_dispatch_queue* q);
+/* DispatchQueue::drop_async (prefill_dispatch.rs:177-187): frees the queue
+ * without waiting (warns on stderr if dispatches are pending); the caller keeps
+ * their buffers alive until a later wait. */
+void t0mi_dq_drop_async(t0mi_dispatch_queue* q);
+/* batch_dispatch (prefill_dispatch.rs:204-214): submit n dispatches
+ * (grids = n x 3 work-item counts) and flush once; *count = n on success. */
+int t0mi_batch_dispatch(t0mi_ctx* ctx, size_t n, const t0mi_kernel* const* kernels, const uint32_t* grids,
+                        const uint8_t* const* kas, const size_t* ka_lens, size_t* count);
+
+/* HIP graphs (no reference counterpart; the MI355X form of batched submission,
+ * prefill_dispatch.rs:1-46): between begin and end, library calls on ctx that
+ * only launch kernels are recorded from ctx's stream instead of run; end
+ * instantiates them, and t0mi_graph_launch replays the batch with one launch
+ * call (asynchronous; wait with t0mi_wait_idle).  While capturing, calls that
+ * wait, allocate, copy to the host or must grow the library workspace return
+ * T0MI_ERR_CAPTURE and leave the capture usable: run a batch once before
+ * capturing it so the workspace has its size.  While a graph is alive the
+ * workspace cannot move (growth returns T0MI_ERR_CAPTURE); destroy graphs
+ * before their runtime.  The runtime's stream must not be the null stream. */
+typedef struct t0mi_graph t0mi_graph;
+int t0mi_capture_begin(t0mi_ctx* ctx);
+int t0mi_capture_end(t0mi_ctx* ctx, t0mi_graph** out);
+int t0mi_graph_launch(t0mi_graph* g);
+size_t t0mi_graph_node_count(const t0mi_graph* g);
+void t0mi_graph_destroy(t0mi_graph* g);
 
 /* ---- tile_ir surface: TileGemm (src/t0/tile_ir.rs:100-152) ---------------- */
 /* EpilogueOp of the tile_ir fusion chain (tile_ir.rs:40-58), applied in order

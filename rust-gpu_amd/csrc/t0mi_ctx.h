@@ -60,6 +60,9 @@ struct t0mi_ctx {
   // from ws, which the GEMMs they launch may use for split-K).
   void* cvt = nullptr;
   size_t cvt_bytes = 0;
+  // Instantiated graphs captured on this runtime: their kernel nodes hold ws
+  // and cvt addresses, so neither buffer may move while one is alive.
+  std::atomic<int> live_graphs{0};
   // Null backend: injected failure and the last recorded dispatch.
   bool inject_timeout = false;
   uint32_t last_grid[3] = {0, 0, 0};
@@ -79,6 +82,13 @@ int run_gemm_auto(t0mi_ctx* ctx, uint32_t transpose, uint64_t x, uint64_t b, uin
 // Launches the bf16 GEMM kernel for (cfg, params) on ctx's stream.
 int launch_gemm(t0mi_ctx* ctx, const t0mi_gemm_config& cfg, const GemmLaunchEntry* e, GemmParams p);
 int check_ctx(t0mi_ctx* ctx);
+// T0MI_ERR_CAPTURE when ctx's stream is being captured into a graph (calls
+// that wait, allocate or copy to the host cannot be recorded); `what` names
+// the refused call.
+int refuse_if_capturing(t0mi_ctx* ctx, const char* what);
+// Fills `bytes` bytes at dst with `value` on ctx's stream, with a kernel (a
+// memset node recorded into a graph has given wrong results on replay).
+int fill_async(t0mi_ctx* ctx, void* dst, uint8_t value, size_t bytes);
 // Sums sk f32 planes of [M, N] (ascending plane order), applies the epilogue
 // chain and stores f32 or bf16 into y (row stride ldy), on ctx's stream.
 int launch_splitk_reduce(t0mi_ctx* ctx, const float* ws, void* y, const float* bias, uint32_t M, uint32_t N,

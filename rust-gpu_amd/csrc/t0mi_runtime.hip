@@ -11,6 +11,7 @@
 // must equal the kernel's declaration, synchronous wait with a timeout that
 // poisons the runtime — and turns it into a hipLaunchKernelGGL on the
 // runtime's stream.
+#include <sched.h>
 #include <string.h>
 #include <time.h>
 
@@ -50,12 +51,64 @@ static int hip_fail(hipError_t e, const char* what) {
   return set_error(T0MI_ERR_HIP, "%s: %s", what, hipGetErrorString(e));
 }
 
+int refuse_if_capturing(t0mi_ctx* ctx, const char* what) {
+  if (ctx->null_backend || !ctx->stream) return T0MI_OK;  // the null stream cannot be captured
+  hipStreamCaptureStatus st = hipStreamCaptureStatusNone;
+  hipError_t e = hipStreamIsCapturing(ctx->stream, &st);
+  if (e != hipSuccess) return hip_fail(e, "hipStreamIsCapturing");
+  if (st != hipStreamCaptureStatusNone)
+    return set_error(T0MI_ERR_CAPTURE, "%s cannot run while the runtime's stream is being captured", what);
+  return T0MI_OK;
+}
+
+// Byte fill: 16-byte stores over the aligned middle, single bytes at the ends.
+__global__ __launch_bounds__(256) void t0mi_fill_kernel(uint8_t* __restrict__ dst, uint32_t word, size_t head,
+                                                        size_t body16, size_t n) {
+  const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x, stride = (size_t)gridDim.x * blockDim.x;
+  const u32x4 q = {word, word, word, word};
+  u32x4* mid = (u32x4*)(dst + head);
+  for (size_t j = i; j < body16; j += stride) mid[j] = q;
+  const size_t tail0 = head + body16 * 16;
+  if (i < head) dst[i] = (uint8_t)word;
+  if (i < n - tail0) dst[tail0 + i] = (uint8_t)word;
+}
+
+int fill_async(t0mi_ctx* ctx, void* dst, uint8_t value, size_t bytes) {
+  if (bytes == 0 || ctx->null_backend) return T0MI_OK;
+  const size_t mis = (uintptr_t)dst & 15;
+  const size_t head = std::min(bytes, mis ? 16 - mis : (size_t)0);
+  const size_t body16 = (bytes - head) / 16;
+  // head and tail are < 16 bytes each, covered by the first workgroup.
+  const size_t blocks = std::max<size_t>(1, std::min<size_t>((body16 + 255) / 256, (size_t)ctx->cu_count * 8));
+  hipLaunchKernelGGL(t0mi_fill_kernel, dim3((uint32_t)blocks), dim3(256), 0, ctx->stream, (uint8_t*)dst,
+                     value * 0x01010101u, head, body16, bytes);
+  hipError_t e = hipGetLastError();
+  return e == hipSuccess ? T0MI_OK : hip_fail(e, "fill launch");
+}
+
+// A buffer that graphs still reference cannot be replaced; one that must grow
+// while the stream is captured cannot be allocated (run the work once eagerly
+// first: the buffers only grow, so a captured replay then fits).
+static int check_growth(t0mi_ctx* ctx, const char* what, size_t have, size_t want) {
+  if (ctx->live_graphs.load() > 0)
+    return set_error(T0MI_ERR_CAPTURE,
+                     "%s must grow from %zu to %zu bytes but %d live graph(s) reference it; destroy them first",
+                     what, have, want, ctx->live_graphs.load());
+  int rc = refuse_if_capturing(ctx, "growing the library workspace");
+  if (rc)
+    set_error(T0MI_ERR_CAPTURE,
+              "%s must grow from %zu to %zu bytes while the stream is captured; run the work once before capturing",
+              what, have, want);
+  return rc;
+}
+
 int ensure_workspace(t0mi_ctx* ctx, size_t bytes) {
   if (ctx->ws_bytes >= bytes) return T0MI_OK;
   if (ctx->null_backend) {
     ctx->ws_bytes = bytes;
     return T0MI_OK;
   }
+  if (int rc = check_growth(ctx, "the split-K workspace", ctx->ws_bytes, bytes)) return rc;
   hipError_t e = hipStreamSynchronize(ctx->stream);
   if (e != hipSuccess) return hip_fail(e, "hipStreamSynchronize");
   if (ctx->ws) (void)hipFree(ctx->ws);
@@ -74,6 +127,7 @@ int ensure_cvt_buffer(t0mi_ctx* ctx, size_t bytes) {
     ctx->cvt_bytes = bytes;
     return T0MI_OK;
   }
+  if (int rc = check_growth(ctx, "the conversion buffer", ctx->cvt_bytes, bytes)) return rc;
   hipError_t e = hipStreamSynchronize(ctx->stream);
   if (e != hipSuccess) return hip_fail(e, "hipStreamSynchronize");
   if (ctx->cvt) (void)hipFree(ctx->cvt);
@@ -275,6 +329,7 @@ extern "C" int t0mi_null_last_dispatch(t0mi_ctx* ctx, uint32_t grid[3], uint8_t*
 extern "C" int t0mi_alloc(t0mi_ctx* ctx, size_t bytes, uint64_t* dptr) {
   if (!ctx || !dptr) return set_error(T0MI_ERR_INVALID, "null argument");
   if (ctx->null_backend) return set_error(T0MI_ERR_NO_DEVICE, "null runtime has no memory");
+  if (int rc = refuse_if_capturing(ctx, "t0mi_alloc")) return rc;
   void* p = nullptr;
   hipError_t e = hipMalloc(&p, bytes ? bytes : 1);
   if (e != hipSuccess) return hip_fail(e, "hipMalloc");
@@ -287,9 +342,10 @@ extern "C" int t0mi_alloc(t0mi_ctx* ctx, size_t bytes, uint64_t* dptr) {
 extern "C" int t0mi_alloc_zero(t0mi_ctx* ctx, size_t bytes, uint64_t* dptr) {
   int rc = t0mi_alloc(ctx, bytes, dptr);
   if (rc) return rc;
-  hipError_t e = hipMemsetAsync((void*)*dptr, 0, bytes, ctx->stream);
-  if (e == hipSuccess) e = hipStreamSynchronize(ctx->stream);
-  return e == hipSuccess ? T0MI_OK : hip_fail(e, "hipMemset");
+  rc = fill_async(ctx, (void*)*dptr, 0, bytes);
+  if (rc) return rc;
+  hipError_t e = hipStreamSynchronize(ctx->stream);
+  return e == hipSuccess ? T0MI_OK : hip_fail(e, "hipStreamSynchronize");
 }
 
 extern "C" int t0mi_free(t0mi_ctx* ctx, uint64_t dptr) {
@@ -297,6 +353,7 @@ extern "C" int t0mi_free(t0mi_ctx* ctx, uint64_t dptr) {
   std::lock_guard<std::mutex> lk(ctx->mu);
   auto it = ctx->allocs.find(dptr);
   if (it == ctx->allocs.end()) return set_error(T0MI_ERR_INVALID, "pointer 0x%llx was not allocated by t0mi_alloc", (unsigned long long)dptr);
+  if (int rc = refuse_if_capturing(ctx, "t0mi_free")) return rc;
   (void)hipStreamSynchronize(ctx->stream);
   hipError_t e = hipFree((void*)dptr);
   ctx->allocs.erase(it);
@@ -305,6 +362,7 @@ extern "C" int t0mi_free(t0mi_ctx* ctx, uint64_t dptr) {
 
 extern "C" int t0mi_h2d(t0mi_ctx* ctx, uint64_t dst, const void* src, size_t bytes) {
   if (!ctx || ctx->null_backend) return set_error(T0MI_ERR_INVALID, "no device runtime");
+  if (int rc = refuse_if_capturing(ctx, "t0mi_h2d")) return rc;
   hipError_t e = hipMemcpyAsync((void*)dst, src, bytes, hipMemcpyHostToDevice, ctx->stream);
   if (e == hipSuccess) e = hipStreamSynchronize(ctx->stream);
   return e == hipSuccess ? T0MI_OK : hip_fail(e, "hipMemcpy H2D");
@@ -312,6 +370,7 @@ extern "C" int t0mi_h2d(t0mi_ctx* ctx, uint64_t dst, const void* src, size_t byt
 
 extern "C" int t0mi_d2h(t0mi_ctx* ctx, void* dst, uint64_t src, size_t bytes) {
   if (!ctx || ctx->null_backend) return set_error(T0MI_ERR_INVALID, "no device runtime");
+  if (int rc = refuse_if_capturing(ctx, "t0mi_d2h")) return rc;
   hipError_t e = hipMemcpyAsync(dst, (const void*)src, bytes, hipMemcpyDeviceToHost, ctx->stream);
   if (e == hipSuccess) e = hipStreamSynchronize(ctx->stream);
   return e == hipSuccess ? T0MI_OK : hip_fail(e, "hipMemcpy D2H");
@@ -319,8 +378,8 @@ extern "C" int t0mi_d2h(t0mi_ctx* ctx, void* dst, uint64_t src, size_t bytes) {
 
 extern "C" int t0mi_memset(t0mi_ctx* ctx, uint64_t dst, int value, size_t bytes) {
   if (!ctx || ctx->null_backend) return set_error(T0MI_ERR_INVALID, "no device runtime");
-  hipError_t e = hipMemsetAsync((void*)dst, value, bytes, ctx->stream);
-  return e == hipSuccess ? T0MI_OK : hip_fail(e, "hipMemsetAsync");
+  if (bytes && !dst) return set_error(T0MI_ERR_INVALID, "null destination");
+  return fill_async(ctx, (void*)dst, (uint8_t)value, bytes);
 }
 
 // --------------------------------------------------------------- kernels ----
@@ -388,6 +447,7 @@ static int wait_stream(t0mi_ctx* ctx) {
     }
     return T0MI_OK;
   }
+  if (int rc = refuse_if_capturing(ctx, "a synchronous wait")) return rc;
   hipEvent_t ev;
   hipError_t e = hipEventCreateWithFlags(&ev, hipEventDisableTiming);
   if (e != hipSuccess) return hip_fail(e, "hipEventCreate");
@@ -414,8 +474,14 @@ static int wait_stream(t0mi_ctx* ctx) {
       rc = set_error(T0MI_ERR_TIMEOUT, "[t0mi] dispatch timed out after %u ms; runtime poisoned", ctx->timeout_ms);
       break;
     }
-    struct timespec sl = {0, 10000};  // 10 us, as aql.rs:486
-    nanosleep(&sl, nullptr);
+    // aql.rs:486 sleeps 10 us per poll; a sleep that short still costs the
+    // kernel's timer slack (~50 us), so the first millisecond only yields.
+    if (ms < 1.0) {
+      sched_yield();
+    } else {
+      struct timespec sl = {0, 10000};
+      nanosleep(&sl, nullptr);
+    }
   }
   if (rc == T0MI_OK) (void)hipEventDestroy(ev);  // a timed-out event is leaked on purpose
   return rc;
@@ -542,7 +608,10 @@ extern "C" int t0mi_dispatch_async(t0mi_ctx* ctx, const t0mi_kernel* k, const ui
 
 extern "C" int t0mi_dispatch(t0mi_ctx* ctx, const t0mi_kernel* k, const uint32_t grid[3], const uint8_t* ka,
                              size_t ka_len) {
-  int rc = dispatch_impl(ctx, k, grid, ka, ka_len);
+  // A synchronous dispatch cannot be recorded: refuse before launching.
+  int rc = ctx ? refuse_if_capturing(ctx, "t0mi_dispatch (synchronous)") : T0MI_OK;
+  if (rc) return rc;
+  rc = dispatch_impl(ctx, k, grid, ka, ka_len);
   if (rc) return rc;
   return wait_stream(ctx);
 }
@@ -588,8 +657,8 @@ int run_gemm(t0mi_ctx* ctx, const t0mi_gemm_config& cfg, const GemmLaunchEntry* 
     if (ctx->null_backend) return T0MI_OK;
     rc = ensure_workspace(ctx, (size_t)m * n * 4);
     if (rc) return rc;
-    hipError_t he = hipMemsetAsync(ctx->ws, 0, (size_t)m * n * 4, ctx->stream);
-    if (he != hipSuccess) return hip_fail(he, "hipMemsetAsync");
+    rc = fill_async(ctx, ctx->ws, 0, (size_t)m * n * 4);
+    if (rc) return rc;
     return launch_splitk_reduce(ctx, (const float*)ctx->ws, (void*)y, (const float*)bias, m, n, n, 1u, p.out_bf16,
                                 epi);
   }

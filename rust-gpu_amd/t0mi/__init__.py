@@ -23,6 +23,7 @@ LIB_PATH = os.path.join(_HERE, "libt0mi.so")
 OK = 0
 ERR_INVALID, ERR_NO_KERNEL, ERR_HIP, ERR_POISONED, ERR_KERNARG, ERR_TIMEOUT, ERR_NOT_FOUND, ERR_NO_DEVICE = \
     -1, -2, -3, -4, -5, -6, -7, -8
+ERR_CAPTURE = -9
 NT, NN = 0, 1
 EPI_STORE_F32, EPI_BIAS_ADD, EPI_BIAS_ADD_RELU = 0, 1, 2
 OUT_F32, OUT_BF16 = 0, 1
@@ -185,6 +186,18 @@ SIGNATURES = {
     "t0mi_dispatch_async": (_I, [_P, _P, ctypes.POINTER(_U32), _P, _SZ]),
     "t0mi_wait_idle": (_I, [_P]),
     "t0mi_gemm": (_I, [_P, _CFG, _U64, _U64, _U64, _U64, _U32, _U32, _U32]),
+    "t0mi_dq_new": (_I, [_P, ctypes.POINTER(_P)]),
+    "t0mi_dq_submit": (_I, [_P, _P, ctypes.POINTER(_U32), _P, _SZ]),
+    "t0mi_dq_flush": (_I, [_P, ctypes.POINTER(_SZ)]),
+    "t0mi_dq_pending": (_SZ, [_P]),
+    "t0mi_dq_drop_async": (None, [_P]),
+    "t0mi_batch_dispatch": (_I, [_P, _SZ, ctypes.POINTER(_P), ctypes.POINTER(_U32), ctypes.POINTER(_P),
+                                 ctypes.POINTER(_SZ), ctypes.POINTER(_SZ)]),
+    "t0mi_capture_begin": (_I, [_P]),
+    "t0mi_capture_end": (_I, [_P, ctypes.POINTER(_P)]),
+    "t0mi_graph_launch": (_I, [_P]),
+    "t0mi_graph_node_count": (_SZ, [_P]),
+    "t0mi_graph_destroy": (None, [_P]),
     "t0mi_tuner_create": (_I, [_CHARP, ctypes.POINTER(_P)]),
     "t0mi_tuner_destroy": (None, [_P]),
     "t0mi_tuner_set_params": (None, [_P, _U32, _U32]),
@@ -443,6 +456,85 @@ class Kernel:
         return buf.value.decode()
 
 
+def _grid3(grid: Sequence[int]):
+    return (ctypes.c_uint32 * 3)(*(list(grid) + [1] * (3 - len(grid))))
+
+
+class DispatchQueue:
+    """``DispatchQueue`` (src/t0/prefill_dispatch.rs:58-187): asynchronous
+    submits on the runtime's stream, one wait at ``flush``."""
+
+    def __init__(self, rt: "Runtime"):
+        h = ctypes.c_void_p()
+        check(lib().t0mi_dq_new(rt.handle, ctypes.byref(h)))
+        self.handle = h
+        self._rt = rt
+
+    def submit(self, kernel: Kernel, grid: Sequence[int], ka: bytes) -> None:
+        buf = (ctypes.c_uint8 * max(1, len(ka))).from_buffer_copy(ka or b"\0")
+        check(lib().t0mi_dq_submit(self.handle, kernel.handle, _grid3(grid), buf, len(ka)))
+
+    def flush(self) -> int:
+        n = ctypes.c_size_t()
+        check(lib().t0mi_dq_flush(self.handle, ctypes.byref(n)))
+        return n.value
+
+    def pending(self) -> int:
+        return lib().t0mi_dq_pending(self.handle)
+
+    def drop_async(self) -> None:
+        if self.handle:
+            lib().t0mi_dq_drop_async(self.handle)
+            self.handle = None
+
+    def __del__(self):
+        try:
+            self.drop_async()
+        except Exception:
+            pass
+
+
+def batch_dispatch(rt: "Runtime", dispatches) -> int:
+    """``batch_dispatch`` (prefill_dispatch.rs:204-214): ``dispatches`` is a
+    sequence of (Kernel, grid, kernarg bytes); submit all, flush once."""
+    n = len(dispatches)
+    kernels = (ctypes.c_void_p * max(1, n))(*[d[0].handle for d in dispatches])
+    grids = (ctypes.c_uint32 * max(3, 3 * n))(*[g for d in dispatches for g in _grid3(d[1])])
+    bufs = [(ctypes.c_uint8 * max(1, len(d[2]))).from_buffer_copy(d[2] or b"\0") for d in dispatches]
+    kas = (ctypes.c_void_p * max(1, n))(*[ctypes.addressof(b) for b in bufs])
+    lens = (ctypes.c_size_t * max(1, n))(*[len(d[2]) for d in dispatches])
+    count = ctypes.c_size_t()
+    check(lib().t0mi_batch_dispatch(rt.handle, n, kernels, grids, kas, lens, ctypes.byref(count)))
+    return count.value
+
+
+class Graph:
+    """A batch of library calls recorded from a runtime's stream (HIP graph);
+    ``launch`` replays it asynchronously on that stream."""
+
+    def __init__(self, handle, rt: "Runtime"):
+        self.handle = handle
+        self._rt = rt
+
+    def launch(self) -> None:
+        check(lib().t0mi_graph_launch(self.handle))
+
+    @property
+    def node_count(self) -> int:
+        return lib().t0mi_graph_node_count(self.handle)
+
+    def destroy(self) -> None:
+        if self.handle:
+            lib().t0mi_graph_destroy(self.handle)
+            self.handle = None
+
+    def __del__(self):
+        try:
+            self.destroy()
+        except Exception:
+            pass
+
+
 class Runtime:
     """``GpuRuntime`` (src/ignis/gpu_context.rs:99-545) over HIP."""
 
@@ -532,13 +624,22 @@ class Runtime:
                                    clamp_max))
 
     def dispatch(self, k: Kernel, grid: Sequence[int], ka: bytes, sync: bool = True) -> int:
-        g = (ctypes.c_uint32 * 3)(*(list(grid) + [1] * (3 - len(grid))))
+        g = _grid3(grid)
         buf = (ctypes.c_uint8 * max(1, len(ka))).from_buffer_copy(ka or b"\0")
         f = lib().t0mi_dispatch if sync else lib().t0mi_dispatch_async
         return f(self.handle, k.handle, g, buf, len(ka))
 
     def wait_idle(self) -> int:
         return lib().t0mi_wait_idle(self.handle)
+
+    # batched submission as a HIP graph
+    def capture_begin(self) -> None:
+        check(lib().t0mi_capture_begin(self.handle))
+
+    def capture_end(self) -> Graph:
+        h = ctypes.c_void_p()
+        check(lib().t0mi_capture_end(self.handle, ctypes.byref(h)))
+        return Graph(h, self)
 
     def gemm(self, cfg: GemmConfig, x: int, b: int, y: int, m: int, n: int, k: int, bias: int = 0) -> None:
         check(lib().t0mi_gemm(self.handle, ctypes.byref(cfg), x, b, y, bias, m, n, k))
