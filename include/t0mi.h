@@ -382,7 +382,8 @@ int t0mi_w4a16_gemm(t0mi_ctx* ctx, uint64_t a, uint64_t qweight, uint64_t scales
 /* Standalone dequant, replacing build_dequant_int4_{f32,bf16} (quant_kernels.rs:53-171)
  * on the same layouts as t0mi_w4a16_gemm: out[k][n] = (float)(q - z) * s.
  * round_mode 0: f32 out; 1: bf16 by truncation (the reference's store_bf16,
- * quant_kernels.rs:167-168); 2: bf16 round-to-nearest-even.  Bit-exact. */
+ * quant_kernels.rs:167-168); 2: bf16 round-to-nearest-even.  Bit-exact.
+ * qweight and an f32 out are 16-byte aligned, scales and a bf16 out 8-byte. */
 int t0mi_dequant_int4(t0mi_ctx* ctx, uint64_t qweight, uint64_t scales, uint64_t qzeros, uint32_t zp_const,
                       uint64_t out, uint32_t k, uint32_t n, uint32_t group, uint32_t round_mode);
 

@@ -699,8 +699,8 @@ extern "C" int t0mi_gemm(t0mi_ctx* ctx, const t0mi_gemm_config* cfg, uint64_t x,
 }
 
 int t0mi::run_gemm_auto(t0mi_ctx* ctx, uint32_t transpose, uint64_t x, uint64_t b, uint64_t y, uint32_t m, uint32_t n,
-                  uint32_t k) {
-  const std::vector<t0mi_gemm_config> cands = rank_candidates(m, n, k, transpose, T0MI_OUT_F32, nullptr);
+                        uint32_t k, uint32_t out_dtype) {
+  const std::vector<t0mi_gemm_config> cands = rank_candidates(m, n, k, transpose, out_dtype, nullptr);
   for (const t0mi_gemm_config& c : cands) {
     const GemmLaunchEntry* e = find_gemm_launch(c);
     if (e) return run_gemm(ctx, c, e, x, b, y, 0, m, n, k, EpiChain{});

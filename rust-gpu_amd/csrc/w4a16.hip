@@ -272,32 +272,53 @@ __global__ __launch_bounds__(WAVES * 64) void w4a16_decode_grouped(W4Params p) {
   }
 }
 
-// Standalone dequant (replaces build_dequant_int4_{f32,bf16}, quant_kernels.rs:53-171):
-// one thread per packed word -> 8 outputs down column n.  round_mode 0: f32,
-// 1: bf16 truncation (the reference's store_bf16), 2: bf16 RNE.
+// Standalone INT4 dequant to [K][N] (replaces build_dequant_int4_{f32,bf16},
+// quant_kernels.rs:53-171, whose addressing is defective): thread (x, y) owns
+// k-octet kk = y and columns n .. n+3 (n = 4x): one 16-byte qweight load, its
+// four bf16 scales and zero points, and eight output rows written as 8-byte
+// (bf16) or 16-byte (f32) row segments, coalesced along N.
+// v = (q - z) * s is exact in fp32; round_mode 0 stores it, 1 truncates to
+// bf16 (the reference's store_bf16), 2 rounds to nearest even.
 __global__ __launch_bounds__(256) void dequant_int4_kernel(const uint32_t* __restrict__ w,
                                                            const uint16_t* __restrict__ scales,
                                                            const uint32_t* __restrict__ zeros, uint32_t zp_const,
                                                            void* __restrict__ out, uint32_t K, uint32_t N,
                                                            uint32_t group, uint32_t round_mode) {
-  const size_t words = (size_t)(K / 8) * N;
-  for (size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x; i < words; i += (size_t)gridDim.x * blockDim.x) {
-    const uint32_t kk = (uint32_t)(i / N), n = (uint32_t)(i % N);
-    const uint32_t word = w[i];
+  const uint32_t n = (blockIdx.x * blockDim.x + threadIdx.x) * 4;
+  if (n >= N) return;  // N % 8 == 0: a thread's four columns are all in range or all out
+  for (uint32_t kk = blockIdx.y; kk < K / 8; kk += gridDim.y) {
+    const u32x4 wq = __builtin_nontemporal_load((const u32x4*)(w + (size_t)kk * N + n));
+    const uint32_t wv[4] = {wq.x, wq.y, wq.z, wq.w};
+    uint32_t gk = kk * 8 / group;
+    u32x2 sv = *(const u32x2*)(scales + (size_t)gk * N + n);
+    uint32_t zw = zeros ? zeros[(size_t)gk * (N / 8) + n / 8] >> (4 * (n & 7)) : 0u;
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
       const uint32_t k = kk * 8 + e;
-      const uint32_t grp = k / group;
-      const int q = (int)((word >> (4 * e)) & 0xFu);
-      const int z = zeros ? (int)((zeros[(size_t)grp * (N / 8) + n / 8] >> (4 * (n & 7))) & 0xFu) : (int)zp_const;
-      const float v = (float)(q - z) * bf16f(scales[(size_t)grp * N + n]);
+      if (group % 8 != 0 && k / group != gk) {  // a group boundary inside the octet
+        gk = k / group;
+        sv = *(const u32x2*)(scales + (size_t)gk * N + n);
+        zw = zeros ? zeros[(size_t)gk * (N / 8) + n / 8] >> (4 * (n & 7)) : 0u;
+      }
+      float v[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int q = (int)((wv[j] >> (4 * e)) & 0xFu);
+        const int z = zeros ? (int)((zw >> (4 * j)) & 0xFu) : (int)zp_const;
+        const uint32_t sb = j < 2 ? sv.x : sv.y;
+        const float sc = __builtin_bit_cast(float, (j & 1) ? (sb & 0xFFFF0000u) : (sb << 16));
+        v[j] = (float)(q - z) * sc;
+      }
       const size_t o = (size_t)k * N + n;
-      if (round_mode == 0)
-        ((float*)out)[o] = v;
-      else if (round_mode == 1)
-        ((uint16_t*)out)[o] = (uint16_t)(__builtin_bit_cast(uint32_t, v) >> 16);
-      else
-        ((uint16_t*)out)[o] = f32_to_bf16_rne(v);
+      if (round_mode == 0) {
+        *(f32x4*)((float*)out + o) = f32x4{v[0], v[1], v[2], v[3]};
+      } else {
+        uint32_t h[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+          h[j] = round_mode == 1 ? __builtin_bit_cast(uint32_t, v[j]) >> 16 : (uint32_t)f32_to_bf16_rne(v[j]);
+        *(u32x2*)((uint16_t*)out + o) = u32x2{h[0] | (h[1] << 16), h[2] | (h[3] << 16)};
+      }
     }
   }
 }
@@ -309,8 +330,21 @@ static int hip_fail(hipError_t e, const char* what) {
 }
 
 // Up to this many rows the decode kernel (16-row slabs) runs; above it the
-// MFMA prefill kernel.
+// MFMA prefill kernel, and from kTwoPassRows rows on the weights are
+// dequantized once to bf16 and the dense NN GEMM runs: the dequant pass
+// (0.5 B read + 2 B written per weight, at HBM speed) then costs less than
+// dequantizing inside every M tile's K-loop.
 static constexpr uint32_t kDecodeMaxRows = 32;
+static constexpr uint32_t kTwoPassRows = 768;
+
+static int launch_dequant(t0mi_ctx* ctx, uint64_t qweight, uint64_t scales, uint64_t qzeros, uint32_t zp_const,
+                          uint64_t out, uint32_t k, uint32_t n, uint32_t group, uint32_t round_mode) {
+  const dim3 grid((n / 4 + 255) / 256, std::min<uint32_t>(k / 8, 65535u));
+  hipLaunchKernelGGL(dequant_int4_kernel, grid, dim3(256), 0, ctx->stream, (const uint32_t*)qweight,
+                     (const uint16_t*)scales, (const uint32_t*)qzeros, zp_const, (void*)out, k, n, group, round_mode);
+  hipError_t e = hipGetLastError();
+  return e == hipSuccess ? T0MI_OK : hip_fail(e, "dequant launch");
+}
 
 extern "C" int t0mi_w4a16_gemm(t0mi_ctx* ctx, uint64_t a, uint64_t qweight, uint64_t scales, uint64_t qzeros,
                                uint32_t zp_const, uint64_t y, uint32_t m, uint32_t k, uint32_t n, uint32_t group,
@@ -340,6 +374,16 @@ extern "C" int t0mi_w4a16_gemm(t0mi_ctx* ctx, uint64_t a, uint64_t qweight, uint
   p.out_bf16 = out_dtype == T0MI_OUT_BF16;
   p.nib_mask = 0x000F000Fu;
   p.nib_magic = 0x43004300u;
+  if (m >= kTwoPassRows) {
+    // W -> bf16 [K][N] (RNE of the exact (q - z) * s: the value the fused
+    // kernels round to as well) in the library's conversion buffer, then the
+    // NN GEMM with the cost model's config for this shape.
+    rc = ensure_cvt_buffer(ctx, (size_t)k * n * 2);
+    if (rc) return rc;
+    rc = launch_dequant(ctx, qweight, scales, qzeros, zp_const, (uint64_t)ctx->cvt, k, n, group, 2);
+    if (rc) return rc;
+    return run_gemm_auto(ctx, T0MI_NN, a, (uint64_t)ctx->cvt, y, m, n, k, out_dtype);
+  }
   if (m > kDecodeMaxRows && (group & (group - 1)) == 0) {
     // Many rows: dequant fused into the MFMA K-loop, weights read once per tile column.
     W4PrefillParams q;
@@ -462,10 +506,7 @@ extern "C" int t0mi_dequant_int4(t0mi_ctx* ctx, uint64_t qweight, uint64_t scale
   if (round_mode > 2) return set_error(T0MI_ERR_INVALID, "round_mode=%u (0 f32, 1 bf16 trunc, 2 bf16 rne)", round_mode);
   if (zp_const > 15) return set_error(T0MI_ERR_INVALID, "zp_const=%u outside 0..15", zp_const);
   if (ctx->null_backend || k == 0 || n == 0) return T0MI_OK;
-  const size_t words = (size_t)(k / 8) * n;
-  const uint32_t blocks = (uint32_t)std::min<size_t>((words + 255) / 256, (size_t)ctx->cu_count * 16);
-  hipLaunchKernelGGL(dequant_int4_kernel, dim3(blocks), dim3(256), 0, ctx->stream, (const uint32_t*)qweight,
-                     (const uint16_t*)scales, (const uint32_t*)qzeros, zp_const, (void*)out, k, n, group, round_mode);
-  hipError_t e = hipGetLastError();
-  return e == hipSuccess ? T0MI_OK : hip_fail(e, "dequant launch");
+  if ((qweight & 15) || (scales & 7) || (out & (round_mode == 0 ? 15 : 7)))
+    return set_error(T0MI_ERR_INVALID, "qweight and an f32 out must be 16-byte aligned, scales and a bf16 out 8-byte");
+  return launch_dequant(ctx, qweight, scales, qzeros, zp_const, out, k, n, group, round_mode);
 }

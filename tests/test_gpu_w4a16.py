@@ -74,11 +74,15 @@ def test_w4a16_vs_oracle(rt, m, k, n, group, pgz):
     (37, 384, 200, 128, True),       # just above the decode range: 128x128 tiles
     (64, 256, 136, 32, True),
     (300, 512, 264, 64, False),      # ragged M and N tiles
-    (1024, 1024, 512, 128, True),    # 256x256 tiles
+    (767, 256, 136, 128, True),      # last row count of the fused kernel
+    (768, 256, 136, 128, True),      # first of the two-pass route (dequant to bf16, dense GEMM)
+    (800, 384, 264, 96, True),       # two-pass with a group that is not a power of two
+    (1024, 1024, 512, 128, True),
     (1100, 384, 520, 128, False),
 ])
 def test_w4a16_prefill_vs_oracle(rt, m, k, n, group, pgz):
-    """Prefill rows: the dequantised weight is rounded to bf16 (RNE) inside the K-loop.
+    """Prefill rows: the dequantised weight is rounded to bf16 (RNE), inside the K-loop
+    (fused kernel) or in a dequant pass before the dense GEMM (from 768 rows on).
     Against the oracle GEMM on RNE(exact dequant) weights the result matches to fp32
     accumulation noise (this pins the in-loop dequant bit for bit up to summation order);
     against the exact-dequant oracle it is within the GEMM tolerance."""
@@ -135,8 +139,9 @@ def test_w4a16_integer_exact(rt):
 
 @pytest.mark.parametrize("round_mode", [0, 1, 2])
 @pytest.mark.parametrize("pgz", [False, True])
-def test_dequant_bit_exact(rt, round_mode, pgz):
-    k, n, group = 512, 264, 128
+@pytest.mark.parametrize("k,n,group", [(512, 264, 128), (48, 72, 12), (96, 8, 32), (256, 2056, 64)])
+def test_dequant_bit_exact(rt, round_mode, pgz, k, n, group):
+    """Group 12 puts group boundaries inside k-octets; N = 2056 leaves a partial workgroup."""
     q = oracle.nibbles((k, n), 31)
     w = oracle.pack_qweight(q)
     s = oracle.uniform_bf16((k // group, n), 32, -0.05, 0.05)
