@@ -329,12 +329,14 @@ static int hip_fail(hipError_t e, const char* what) {
   return set_error(T0MI_ERR_HIP, "%s: %s", what, hipGetErrorString(e));
 }
 
-// Up to this many rows the decode kernel (16-row slabs) runs; above it the
-// MFMA prefill kernel, and from kTwoPassRows rows on the weights are
-// dequantized once to bf16 and the dense NN GEMM runs: the dequant pass
-// (0.5 B read + 2 B written per weight, at HBM speed) then costs less than
-// dequantizing inside every M tile's K-loop.
-static constexpr uint32_t kDecodeMaxRows = 32;
+// Up to this many rows the decode kernel runs once per 16-row slab (measured
+// at K = 4096, N = 11008 and 14336: 7 slabs cost less than one launch of the
+// fused kernel, whose K-loop is latency-bound at small M); above it the MFMA
+// prefill kernel, and from kTwoPassRows rows on the weights are dequantized
+// once to bf16 and the dense NN GEMM runs: the dequant pass (0.5 B read + 2 B
+// written per weight, at HBM speed) then costs less than dequantizing inside
+// every M tile's K-loop.
+static constexpr uint32_t kDecodeMaxRows = 112;
 static constexpr uint32_t kTwoPassRows = 768;
 
 static int launch_dequant(t0mi_ctx* ctx, uint64_t qweight, uint64_t scales, uint64_t qzeros, uint32_t zp_const,
