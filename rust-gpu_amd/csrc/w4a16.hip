@@ -330,13 +330,13 @@ static int hip_fail(hipError_t e, const char* what) {
 }
 
 // Up to this many rows the decode kernel runs once per 16-row slab (measured
-// at K = 4096, N = 11008 and 14336: 7 slabs cost less than one launch of the
-// fused kernel, whose K-loop is latency-bound at small M); above it the MFMA
+// at K = 4096, N = 11008 and 14336: 5 slabs cost about one launch of the
+// fused kernel, whose dequant work per workgroup does not shrink with M); above it the MFMA
 // prefill kernel, and from kTwoPassRows rows on the weights are dequantized
 // once to bf16 and the dense NN GEMM runs: the dequant pass (0.5 B read + 2 B
 // written per weight, at HBM speed) then costs less than dequantizing inside
 // every M tile's K-loop.
-static constexpr uint32_t kDecodeMaxRows = 112;
+static constexpr uint32_t kDecodeMaxRows = 80;
 static constexpr uint32_t kTwoPassRows = 768;
 
 static int launch_dequant(t0mi_ctx* ctx, uint64_t qweight, uint64_t scales, uint64_t qzeros, uint32_t zp_const,
@@ -402,22 +402,33 @@ extern "C" int t0mi_w4a16_gemm(t0mi_ctx* ctx, uint64_t a, uint64_t qweight, uint
     q.zp_const = zp_const;
     q.out_bf16 = p.out_bf16;
     q.xcd_remap = 1;
-    const bool big = m >= 1024;
-    const uint32_t bm = big ? 256 : 128, bn = big ? 256 : 128;
-    q.tiles_m = (m + bm - 1) / bm;
-    q.tiles_n = (n + bn - 1) / bn;
-    const dim3 grid(q.tiles_n, q.tiles_m);
-    const bool z = qzeros != 0;
-    if (big) {
-      if (z)
-        hipLaunchKernelGGL((w4a16_prefill_kernel<256, 256, 64, 2, 4, true>), grid, dim3(512), 0, ctx->stream, q);
-      else
-        hipLaunchKernelGGL((w4a16_prefill_kernel<256, 256, 64, 2, 4, false>), grid, dim3(512), 0, ctx->stream, q);
-    } else {
-      if (z)
-        hipLaunchKernelGGL((w4a16_prefill_kernel<128, 128, 64, 2, 2, true>), grid, dim3(256), 0, ctx->stream, q);
-      else
-        hipLaunchKernelGGL((w4a16_prefill_kernel<128, 128, 64, 2, 2, false>), grid, dim3(256), 0, ctx->stream, q);
+    // 128x128 tiles (rows 113..767: at most 6 tile rows), 4 tiles in flight.
+    // With fewer tiles than CUs, K is split so that every CU dequantizes a
+    // share of the weights; the partitions' f32 planes are then summed in
+    // partition order (deterministic) by the split-K reduce.
+    q.tiles_m = (m + 127) / 128;
+    q.tiles_n = (n + 127) / 128;
+    const uint32_t tiles = q.tiles_m * q.tiles_n, nk_all = (k + 63) / 64;
+    uint32_t sk = std::max(1u, std::min(4u, (uint32_t)ctx->cu_count / std::max(1u, tiles)));
+    sk = std::min(sk, nk_all);
+    q.kt_per_split = (nk_all + sk - 1) / sk;
+    sk = (nk_all + q.kt_per_split - 1) / q.kt_per_split;  // no empty partition
+    const size_t plane = (size_t)m * n * 4;
+    if (sk > 1) {
+      rc = ensure_workspace(ctx, plane * sk);
+      if (rc) return rc;
+      q.y = ctx->ws;
+      q.y_split_stride = plane;
+    }
+    const dim3 grid(q.tiles_n, q.tiles_m * sk);
+    if (qzeros)
+      hipLaunchKernelGGL((w4a16_prefill_kernel<128, 128, 64, 2, 2, 4, true>), grid, dim3(256), 0, ctx->stream, q);
+    else
+      hipLaunchKernelGGL((w4a16_prefill_kernel<128, 128, 64, 2, 2, 4, false>), grid, dim3(256), 0, ctx->stream, q);
+    if (sk > 1) {
+      hipError_t le = hipGetLastError();
+      if (le != hipSuccess) return hip_fail(le, "w4a16 prefill launch");
+      return launch_splitk_reduce(ctx, (const float*)ctx->ws, (void*)y, nullptr, m, n, n, sk, p.out_bf16, EpiChain{});
     }
     hipError_t e = hipGetLastError();
     return e == hipSuccess ? T0MI_OK : hip_fail(e, "w4a16 prefill launch");

@@ -8,15 +8,19 @@
 //   scales  bf16 [K/g][N]; zeros u32 [K/g][N/8] (nibble e = column 8j+e) or a constant.
 //
 // Weights cross HBM once, at 4 bits.  Per K tile:
-//   * A goes global -> LDS by DMA exactly as in gemm_bf16_kernel (swizzled
-//     K-contiguous rows);
-//   * B arrives one tile ahead as packed words in registers: thread t owns one
-//     k-octet r and four consecutive columns, i.e. one 16-byte load per tile
-//     (a wave reads one 1 KB row of qweight: coalesced along N);
-//   * during the MFMAs of tile it, each thread dequantises its four words of
-//     tile it+1 — (q - z) * s exactly in fp32, rounded once to bf16 (RNE) —
-//     and writes them as the swizzled K-contiguous [BN][BK] LDS tile that the
-//     NT fragment reads use.
+//   * A arrives in registers (16-byte loads, the same swizzled K-contiguous
+//     1 KB LDS blocks the GEMM's DMA fills) and B as packed words: thread t
+//     owns one k-octet r and four consecutive columns, i.e. one 16-byte load
+//     per tile (a wave reads one 1 KB row of qweight: coalesced along N);
+//   * both are requested S-1 tiles ahead into a ring of S register sets, so
+//     S-1 tiles are in flight while one is computed.  At small M a tile's
+//     MFMA work is far shorter than the memory latency, and the latency, not
+//     the bandwidth, sets the speed; every load is compiler-tracked, so each
+//     register set is waited for exactly when it is consumed;
+//   * during the MFMAs of tile it, each thread writes tile it+1's A into the
+//     other LDS stage and dequantises its four words of tile it+1 — (q - z) * s
+//     exactly in fp32, rounded once to bf16 (RNE) — into the swizzled
+//     K-contiguous [BN][BK] B tile that the NT fragment reads use.
 // Prefill takes power-of-two group sizes (group index = k >> log2 g).
 // The bf16 rounding of the dequantised weight is the only difference from an
 // exact-dequant GEMM; it is the same value t0mi_dequant_int4 produces with
@@ -34,6 +38,8 @@ struct W4PrefillParams {
   void* y;                 // [M, N] f32 or bf16
   uint32_t M, N, K, group_shift, zp_const, out_bf16;  // group = 1 << group_shift
   uint32_t tiles_m, tiles_n, xcd_remap;
+  uint32_t kt_per_split;    // K tiles per partition (grid = tiles x partitions)
+  uint64_t y_split_stride;  // > 0: partition p stores raw f32 sums at y + p * stride
 };
 
 // Packed B of one thread for one K tile: four columns' words plus their scales
@@ -44,18 +50,21 @@ struct W4Regs {
   uint32_t z;   // qzeros word holding the four columns' zero points
 };
 
-template <int BM, int BN, int BK, int WM, int WN, bool ZEROS>
+template <int BM, int BN, int BK, int WM, int WN, int S, bool ZEROS>
 __global__ __launch_bounds__(WM * WN * 64) void w4a16_prefill_kernel(W4PrefillParams p) {
   constexpr int NWAVES = WM * WN, NTHR = NWAVES * 64;
   constexpr int TM = BM / WM, TN = BN / WN, FM = TM / 32, FN = TN / 32;
   constexpr int KC = BK / 8, KS = BK / 16;
   constexpr int A_ELEMS = BM * BK, B_ELEMS = BN * BK, BUF = A_ELEMS + B_ELEMS;
   constexpr int A_BLOCKS = A_ELEMS * 2 / 1024;
-  constexpr int COLQ = BN / 4;  // 4-column groups per tile row
+  constexpr int APT = A_BLOCKS / NWAVES;  // 16-byte A loads per thread per tile
+  constexpr int COLQ = BN / 4;            // 4-column groups per tile row
   static_assert(TM % 32 == 0 && TN % 32 == 0, "wave tile must be a multiple of 32x32");
   static_assert(BK == 32 || BK == 64, "tile_k 32 or 64");
   static_assert(NTHR == COLQ * KC, "one 16-byte word group per thread per K tile");
   static_assert(KS >= 2 && KS <= 4, "the four words of a thread are spread over the k-steps");
+  static_assert(A_BLOCKS % NWAVES == 0, "every thread loads the same number of A chunks");
+  static_assert(S >= 2 && S <= 6, "2..6 tiles in the register ring");
 
   __shared__ __attribute__((aligned(1024))) uint16_t smem[2 * BUF];
 
@@ -65,26 +74,27 @@ __global__ __launch_bounds__(WM * WN * 64) void w4a16_prefill_kernel(W4PrefillPa
   const int wm = wave / WN, wn = wave % WN;
   const int m0 = tm * BM, n0 = tn * BN;
   const int K = (int)p.K;
-  const int nk = (K + BK - 1) / BK;
+  // This partition's K tiles: [kt0, kt0 + nk).
+  const int nk_all = (K + BK - 1) / BK;
+  const int kt0 = part * (int)p.kt_per_split;
+  const int nk = min(nk_all - kt0, (int)p.kt_per_split);
 
-  const int wave_s = __builtin_amdgcn_readfirstlane(wave);
-  const uint32_t smem_base = lds_addr(smem);
-  auto load_a = [&](int k0, int stage) {
-    const uint32_t a_lds = smem_base + (uint32_t)(stage * BUF * 2);
-#pragma unroll
-    for (int j = 0; j < (A_BLOCKS + NWAVES - 1) / NWAVES; ++j) {
-      const int blk = wave_s + j * NWAVES;
-      if (A_BLOCKS % NWAVES != 0 && blk >= A_BLOCKS) break;
-      const int q = blk * 64 + lane;
-      const int row = q / KC, pc = q % KC;
-      const int lc = pc ^ swz<KC>(row);
-      int gr = m0 + row;
-      gr = gr < (int)p.M ? gr : (int)p.M - 1;
-      const int gk = k0 + lc * 8;
-      const void* src = gk < K ? (const void*)(p.a + (size_t)gr * K + gk) : (const void*)g_zero16;
-      lds_dma16(src, a_lds + blk * 1024);
-    }
+  // One tile's registers: this thread's A chunks and packed B words.
+  struct TileRegs {
+    u32x4 a[APT];
+    W4Regs b;
   };
+  // A chunk j of this thread: LDS block blk = wave + j * NWAVES, slot `lane`,
+  // holding row `row`, 16-byte chunk `lc` (swizzled) of the K-contiguous tile.
+  int a_row[APT], a_lc[APT];
+#pragma unroll
+  for (int j = 0; j < APT; ++j) {
+    const int q = (wave + j * NWAVES) * 64 + lane;
+    const int row = q / KC, pc = q % KC;
+    a_lc[j] = pc ^ swz<KC>(row);
+    const int gr = m0 + row;
+    a_row[j] = gr < (int)p.M ? gr : (int)p.M - 1;
+  }
 
   // This thread's slot in the packed B tile.
   const int br = tid / COLQ;           // k-octet within the tile (= logical 16-byte chunk)
@@ -96,12 +106,35 @@ __global__ __launch_bounds__(WM * WN * 64) void w4a16_prefill_kernel(W4PrefillPa
   const int ko_last = K / 8 - 1;
   auto load_b = [&](int k0, W4Regs& r) {
     const int ko = min(k0 / 8 + br, ko_last);  // qweight row
-    r.w = *(const u32x4*)(p.w + (size_t)ko * p.N + gn);
+    r.w = __builtin_nontemporal_load((const u32x4*)(p.w + (size_t)ko * p.N + gn));
     const uint32_t g = (uint32_t)(ko * 8) >> p.group_shift;
     r.s = *(const u32x2*)(p.scales + (size_t)g * p.N + gn);
-    // Used only when the tile is dequantised, so the load stays in flight
-    // across the MFMAs of the current tile.
     if constexpr (ZEROS) r.z = p.zeros[(size_t)g * (p.N / 8) + (uint32_t)gn / 8];
+  };
+  auto load_tile = [&](int t, TileRegs& r) {
+    const int k0 = (kt0 + t) * BK;
+#pragma unroll
+    for (int j = 0; j < APT; ++j) {
+      // Chunks past K read column 0 of the row instead (a global address either
+      // way: a select between A and another buffer would make the pointer
+      // generic, and flat loads are waited for all together); put_a zeroes them.
+      const int gk = k0 + a_lc[j] * 8;
+      r.a[j] = *(const u32x4*)(p.a + (size_t)a_row[j] * K + (gk < K ? gk : 0));
+    }
+    load_b(k0, r.b);
+  };
+  auto put_a = [&](const TileRegs& r, int t, int stage) {
+    uint16_t* As = smem + stage * BUF;
+#pragma unroll
+    for (int j = 0; j < APT; ++j) {
+      // The empty asm pins the zeroing here: without it the compiler moves the
+      // select next to the load (the same condition), which then has to wait
+      // for the load as soon as it is issued.
+      u32x4 v = r.a[j];
+      asm volatile("" : "+v"(v));
+      if ((kt0 + t) * BK + a_lc[j] * 8 >= K) v = (u32x4){0u, 0u, 0u, 0u};
+      *(u32x4*)(As + (wave + j * NWAVES) * 512 + lane * 8) = v;
+    }
   };
   // Dequantise column j of r into its 16-byte LDS chunk of stage `stage`.
   // A nibble pair becomes the bf16 pair (128 + q) with one and/or (exact),
@@ -158,27 +191,36 @@ __global__ __launch_bounds__(WM * WN * 64) void w4a16_prefill_kernel(W4PrefillPa
 #pragma unroll
       for (int e = 0; e < 16; ++e) acc[fn][fm][e] = 0.0f;
 
-  // Prologue: tile 0 in stage 0 (A by DMA, B dequantised from registers), the
-  // packed words of tile 1 requested.
-  W4Regs cur, nxt;
-  if (nk > 0) {
-    load_a(0, 0);
-    load_b(0, cur);
-    wait_vmcnt<0>();
+  // Ring slot u holds tile it0 + u (it0 a multiple of S): the loop below is
+  // unrolled S times so that every slot index is a compile-time constant.
+  // Every iteration requests one tile (past the last tile, the last one again,
+  // never used): the number of loads in flight is then the same on every path
+  // and the compiler waits for each register set exactly, not for all loads.
+  TileRegs ring[S];
+  if (nk <= 0) return;  // the host sizes partitions so that none is empty (K == 0 never launches)
+  // Prologue: tiles 0 .. S-2 requested; tile 0 written to stage 0.
 #pragma unroll
-    for (int j = 0; j < 4; ++j) put_b(cur, j, 0);
-    if (nk > 1) load_b(BK, cur);
-  }
-  for (int it = 0; it < nk; ++it) {
+  for (int t = 0; t < S - 1; ++t) load_tile(min(t, nk - 1), ring[t]);
+  put_a(ring[0], 0, 0);
+#pragma unroll
+  for (int j = 0; j < 4; ++j) put_b(ring[0].b, j, 0);
+  // FULL: a main-loop iteration, where tile it+1 always exists (no branch).
+  auto iteration = [&](auto uc, auto full_c, int it) {
+    constexpr int u = decltype(uc)::value;
+    constexpr bool FULL = decltype(full_c)::value;
     const int c = it & 1;
-    // Tile it's A DMA and tile it+1's packed words have landed; the barrier
-    // publishes tile it (every wave's DMA and dequant writes) and frees stage
-    // c^1, computed in iteration it-1.
-    wait_vmcnt<0>();
+    // Publishes stage c (written during iteration it-1 or the prologue) and
+    // proves every wave is done reading stage c^1 (iteration it-1).  The
+    // scheduling barriers keep each iteration's work inside it: hoisted into
+    // an earlier iteration, the dequant of a tile waits for loads that are
+    // meant to be still in flight.
+    __builtin_amdgcn_sched_barrier(0);
     __syncthreads();
-    const bool more = it + 1 < nk;
-    if (more) load_a((it + 1) * BK, c ^ 1);
-    if (it + 2 < nk) load_b((it + 2) * BK, nxt);
+    load_tile(min(it + S - 1, nk - 1), ring[(u + S - 1) % S]);
+    __builtin_amdgcn_sched_barrier(0);
+    const bool more = FULL || it + 1 < nk;
+    const TileRegs& nx = ring[(u + 1) % S];
+    if (more) put_a(nx, it + 1, c ^ 1);
     const uint16_t* As = smem + c * BUF;
     bf16x8 xa[2][FM], xb[2][FN];
     read_frags(As, 0, xa[0], xb[0]);
@@ -194,11 +236,17 @@ __global__ __launch_bounds__(WM * WN * 64) void w4a16_prefill_kernel(W4PrefillPa
       // Tile it+1's B: 4 / KS columns per k-step, between this k-step's MFMAs.
       if (more) {
 #pragma unroll
-        for (int j = ks * (4 / KS); j < (ks + 1) * (4 / KS); ++j) put_b(cur, j, c ^ 1);
+        for (int j = ks * (4 / KS); j < (ks + 1) * (4 / KS); ++j) put_b(nx.b, j, c ^ 1);
       }
     }
-    cur = nxt;
-  }
+  };
+  int it0 = 0;
+  for (; it0 + S < nk; it0 += S)
+    static_for<S>([&](auto uc) { iteration(uc, std::true_type{}, it0 + decltype(uc)::value); });
+  // The last 1 .. S tiles.
+  static_for<S>([&](auto uc) {
+    if (it0 + decltype(uc)::value < nk) iteration(uc, std::false_type{}, it0 + decltype(uc)::value);
+  });
 
   // Epilogue (as gemm_bf16_kernel): four consecutive columns per (lane, g).
 #pragma unroll
@@ -213,7 +261,10 @@ __global__ __launch_bounds__(WM * WN * 64) void w4a16_prefill_kernel(W4PrefillPa
         if (n >= (int)p.N) continue;
         const float v0 = acc[fn][fm][g * 4 + 0], v1 = acc[fn][fm][g * 4 + 1];
         const float v2 = acc[fn][fm][g * 4 + 2], v3 = acc[fn][fm][g * 4 + 3];
-        if (p.out_bf16) {
+        if (p.y_split_stride) {  // partition plane: raw f32 sums, summed by the reduce pass
+          float* yp = (float*)((char*)p.y + (size_t)part * p.y_split_stride);
+          *(f32x4*)(yp + (size_t)m * p.N + n) = f32x4{v0, v1, v2, v3};
+        } else if (p.out_bf16) {
           u32x2 o;
           o.x = (uint32_t)f32_to_bf16_rne(v0) | ((uint32_t)f32_to_bf16_rne(v1) << 16);
           o.y = (uint32_t)f32_to_bf16_rne(v2) | ((uint32_t)f32_to_bf16_rne(v3) << 16);

@@ -58,8 +58,8 @@ def check(y, ref, a, wf, k, rel_max):
     (16, 1024, 520, 64, True),
     (16, 8192, 256, 128, False),     # K beyond one workgroup's range -> split + reduce
     (32, 384, 200, 128, True),       # M > 16 -> several row slabs
-    (100, 256, 136, 64, False),      # 7 slabs, the last one 4 rows
-    (112, 384, 200, 128, True),      # the largest row count the slabs take
+    (76, 256, 136, 64, False),       # 5 slabs, the last one 12 rows
+    (80, 384, 200, 128, True),       # the largest row count the slabs take
     (70, 384, 136, 96, True),        # slabs with a group that is not a power of two
     (3, 4096, 64, 4096, False),      # group larger than a wave's K range
 ])
@@ -74,9 +74,10 @@ def test_w4a16_vs_oracle(rt, m, k, n, group, pgz):
 
 
 @pytest.mark.parametrize("m,k,n,group,pgz", [
-    (113, 384, 200, 128, True),      # just above the decode-slab range: 128x128 tiles
+    (81, 384, 200, 128, True),       # just above the decode-slab range: 128x128 tiles, split K
     (130, 256, 136, 32, True),
     (300, 512, 264, 64, False),      # ragged M and N tiles
+    (200, 352, 136, 32, True),       # K % 64 == 32: the last K tile is half past K
     (767, 256, 136, 128, True),      # last row count of the fused kernel
     (768, 256, 136, 128, True),      # first of the two-pass route (dequant to bf16, dense GEMM)
     (800, 384, 264, 96, True),       # two-pass with a group that is not a power of two
