@@ -402,7 +402,8 @@ extern "C" int t0mi_w4a16_gemm(t0mi_ctx* ctx, uint64_t a, uint64_t qweight, uint
     q.zp_const = zp_const;
     q.out_bf16 = p.out_bf16;
     q.xcd_remap = 1;
-    // 128x128 tiles (rows 113..767: at most 6 tile rows), 4 tiles in flight.
+    // 128x128 tiles, 8 waves (two per SIMD, so that one wave's dequant runs
+    // beside the other's MFMAs), 4 tiles in flight.
     // With fewer tiles than CUs, K is split so that every CU dequantizes a
     // share of the weights; the partitions' f32 planes are then summed in
     // partition order (deterministic) by the split-K reduce.
@@ -422,9 +423,9 @@ extern "C" int t0mi_w4a16_gemm(t0mi_ctx* ctx, uint64_t a, uint64_t qweight, uint
     }
     const dim3 grid(q.tiles_n, q.tiles_m * sk);
     if (qzeros)
-      hipLaunchKernelGGL((w4a16_prefill_kernel<128, 128, 64, 2, 2, 4, true>), grid, dim3(256), 0, ctx->stream, q);
+      hipLaunchKernelGGL((w4a16_prefill_kernel<128, 128, 64, 2, 4, 4, true>), grid, dim3(512), 0, ctx->stream, q);
     else
-      hipLaunchKernelGGL((w4a16_prefill_kernel<128, 128, 64, 2, 2, 4, false>), grid, dim3(256), 0, ctx->stream, q);
+      hipLaunchKernelGGL((w4a16_prefill_kernel<128, 128, 64, 2, 4, 4, false>), grid, dim3(512), 0, ctx->stream, q);
     if (sk > 1) {
       hipError_t le = hipGetLastError();
       if (le != hipSuccess) return hip_fail(le, "w4a16 prefill launch");

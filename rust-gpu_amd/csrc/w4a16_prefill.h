@@ -10,15 +10,15 @@
 // Weights cross HBM once, at 4 bits.  Per K tile:
 //   * A arrives in registers (16-byte loads, the same swizzled K-contiguous
 //     1 KB LDS blocks the GEMM's DMA fills) and B as packed words: thread t
-//     owns one k-octet r and four consecutive columns, i.e. one 16-byte load
-//     per tile (a wave reads one 1 KB row of qweight: coalesced along N);
+//     owns one k-octet r and CPT (2 or 4) consecutive columns, i.e. one 8- or
+//     16-byte load per tile (coalesced along N);
 //   * both are requested S-1 tiles ahead into a ring of S register sets, so
 //     S-1 tiles are in flight while one is computed.  At small M a tile's
 //     MFMA work is far shorter than the memory latency, and the latency, not
 //     the bandwidth, sets the speed; every load is compiler-tracked, so each
 //     register set is waited for exactly when it is consumed;
 //   * during the MFMAs of tile it, each thread writes tile it+1's A into the
-//     other LDS stage and dequantises its four words of tile it+1 — (q - z) * s
+//     other LDS stage and dequantises its CPT words of tile it+1 — (q - z) * s
 //     exactly in fp32, rounded once to bf16 (RNE) — into the swizzled
 //     K-contiguous [BN][BK] B tile that the NT fragment reads use.
 // Prefill takes power-of-two group sizes (group index = k >> log2 g).
@@ -42,12 +42,14 @@ struct W4PrefillParams {
   uint64_t y_split_stride;  // > 0: partition p stores raw f32 sums at y + p * stride
 };
 
-// Packed B of one thread for one K tile: four columns' words plus their scales
-// and zero points.
+// Packed B of one thread for one K tile: CPT (2 or 4) consecutive columns'
+// words for one k-octet, their bf16 scales (two per word) and the qzeros word
+// holding their zero points.
+template <int CPT>
 struct W4Regs {
-  u32x4 w;      // words of columns n..n+3 for k-octet r
-  u32x2 s;      // bf16 scales of columns n..n+3
-  uint32_t z;   // qzeros word holding the four columns' zero points
+  uint32_t w[CPT];
+  uint32_t s[CPT / 2];
+  uint32_t z;
 };
 
 template <int BM, int BN, int BK, int WM, int WN, int S, bool ZEROS>
@@ -58,11 +60,11 @@ __global__ __launch_bounds__(WM * WN * 64) void w4a16_prefill_kernel(W4PrefillPa
   constexpr int A_ELEMS = BM * BK, B_ELEMS = BN * BK, BUF = A_ELEMS + B_ELEMS;
   constexpr int A_BLOCKS = A_ELEMS * 2 / 1024;
   constexpr int APT = A_BLOCKS / NWAVES;  // 16-byte A loads per thread per tile
-  constexpr int COLQ = BN / 4;            // 4-column groups per tile row
+  constexpr int CPT = BN * KC / NTHR;     // columns (packed words) per thread per K tile
+  constexpr int COLQ = BN / CPT;          // CPT-column groups per tile row
   static_assert(TM % 32 == 0 && TN % 32 == 0, "wave tile must be a multiple of 32x32");
   static_assert(BK == 32 || BK == 64, "tile_k 32 or 64");
-  static_assert(NTHR == COLQ * KC, "one 16-byte word group per thread per K tile");
-  static_assert(KS >= 2 && KS <= 4, "the four words of a thread are spread over the k-steps");
+  static_assert((CPT == 2 || CPT == 4) && NTHR * CPT == BN * KC, "2 or 4 packed words per thread per K tile");
   static_assert(A_BLOCKS % NWAVES == 0, "every thread loads the same number of A chunks");
   static_assert(S >= 2 && S <= 6, "2..6 tiles in the register ring");
 
@@ -82,7 +84,7 @@ __global__ __launch_bounds__(WM * WN * 64) void w4a16_prefill_kernel(W4PrefillPa
   // One tile's registers: this thread's A chunks and packed B words.
   struct TileRegs {
     u32x4 a[APT];
-    W4Regs b;
+    W4Regs<CPT> b;
   };
   // A chunk j of this thread: LDS block blk = wave + j * NWAVES, slot `lane`,
   // holding row `row`, 16-byte chunk `lc` (swizzled) of the K-contiguous tile.
@@ -98,17 +100,25 @@ __global__ __launch_bounds__(WM * WN * 64) void w4a16_prefill_kernel(W4PrefillPa
 
   // This thread's slot in the packed B tile.
   const int br = tid / COLQ;           // k-octet within the tile (= logical 16-byte chunk)
-  const int bc = (tid % COLQ) * 4;     // first of four columns within the tile
+  const int bc = (tid % COLQ) * CPT;   // first of CPT columns within the tile
   // Columns past N and k-octets past K are clamped onto real data: the
   // columns are never stored and the A operand is zero past K, so the loads
   // need no predicate.
-  const int gn = min(n0 + bc, (int)p.N - 4);  // N % 8 == 0
+  const int gn = min(n0 + bc, (int)p.N - CPT);  // N % 8 == 0
   const int ko_last = K / 8 - 1;
-  auto load_b = [&](int k0, W4Regs& r) {
+  auto load_b = [&](int k0, W4Regs<CPT>& r) {
     const int ko = min(k0 / 8 + br, ko_last);  // qweight row
-    r.w = __builtin_nontemporal_load((const u32x4*)(p.w + (size_t)ko * p.N + gn));
     const uint32_t g = (uint32_t)(ko * 8) >> p.group_shift;
-    r.s = *(const u32x2*)(p.scales + (size_t)g * p.N + gn);
+    if constexpr (CPT == 4) {
+      const u32x4 w = __builtin_nontemporal_load((const u32x4*)(p.w + (size_t)ko * p.N + gn));
+      const u32x2 sc = *(const u32x2*)(p.scales + (size_t)g * p.N + gn);
+      r.w[0] = w.x, r.w[1] = w.y, r.w[2] = w.z, r.w[3] = w.w;
+      r.s[0] = sc.x, r.s[1] = sc.y;
+    } else {
+      const u32x2 w = __builtin_nontemporal_load((const u32x2*)(p.w + (size_t)ko * p.N + gn));
+      r.w[0] = w.x, r.w[1] = w.y;
+      r.s[0] = *(const uint32_t*)(p.scales + (size_t)g * p.N + gn);
+    }
     if constexpr (ZEROS) r.z = p.zeros[(size_t)g * (p.N / 8) + (uint32_t)gn / 8];
   };
   auto load_tile = [&](int t, TileRegs& r) {
@@ -142,9 +152,9 @@ __global__ __launch_bounds__(WM * WN * 64) void w4a16_prefill_kernel(W4PrefillPa
   //   fma(128 + q, s, -(128 + z) * s) = (q - z) * s
   // is exact: both products have at most 16 significant bits and the result
   // at most 12.  It is then rounded once to bf16.
-  auto put_b = [&](const W4Regs& r, int j, int stage) {
-    const uint32_t wj = j == 0 ? r.w.x : j == 1 ? r.w.y : j == 2 ? r.w.z : r.w.w;
-    const uint32_t sb = j < 2 ? r.s.x : r.s.y;
+  auto put_b = [&](const W4Regs<CPT>& r, int j, int stage) {
+    const uint32_t wj = r.w[j];
+    const uint32_t sb = r.s[j / 2];
     const float s = __builtin_bit_cast(float, (j & 1) ? (sb & 0xFFFF0000u) : (sb << 16));
     const float zb = (float)((ZEROS ? (r.z >> (4 * ((gn & 7) + j))) & 0xFu : p.zp_const) + 128u);
     const float c = -zb * s;
@@ -203,7 +213,7 @@ __global__ __launch_bounds__(WM * WN * 64) void w4a16_prefill_kernel(W4PrefillPa
   for (int t = 0; t < S - 1; ++t) load_tile(min(t, nk - 1), ring[t]);
   put_a(ring[0], 0, 0);
 #pragma unroll
-  for (int j = 0; j < 4; ++j) put_b(ring[0].b, j, 0);
+  for (int j = 0; j < CPT; ++j) put_b(ring[0].b, j, 0);
   // FULL: a main-loop iteration, where tile it+1 always exists (no branch).
   auto iteration = [&](auto uc, auto full_c, int it) {
     constexpr int u = decltype(uc)::value;
@@ -233,10 +243,12 @@ __global__ __launch_bounds__(WM * WN * 64) void w4a16_prefill_kernel(W4PrefillPa
 #pragma unroll
         for (int fm = 0; fm < FM; ++fm)
           acc[fn][fm] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(xb[cc][fn], xa[cc][fm], acc[fn][fm], 0, 0, 0);
-      // Tile it+1's B: 4 / KS columns per k-step, between this k-step's MFMAs.
+      // Tile it+1's B: column j during k-step j * KS / CPT, between this
+      // k-step's MFMAs.
       if (more) {
 #pragma unroll
-        for (int j = ks * (4 / KS); j < (ks + 1) * (4 / KS); ++j) put_b(nx.b, j, c ^ 1);
+        for (int j = 0; j < CPT; ++j)
+          if (j * KS / CPT == ks) put_b(nx.b, j, c ^ 1);
       }
     }
   };
