@@ -376,7 +376,8 @@ extern "C" int t0mi_w4a16_gemm(t0mi_ctx* ctx, uint64_t a, uint64_t qweight, uint
   p.out_bf16 = out_dtype == T0MI_OUT_BF16;
   p.nib_mask = 0x000F000Fu;
   p.nib_magic = 0x43004300u;
-  if (m >= kTwoPassRows) {
+  const bool pow2_group = (group & (group - 1)) == 0;
+  if (m >= kTwoPassRows || (m > kDecodeMaxRows && !pow2_group)) {
     // W -> bf16 [K][N] (RNE of the exact (q - z) * s: the value the fused
     // kernels round to as well) in the library's conversion buffer, then the
     // NN GEMM with the cost model's config for this shape.
@@ -386,7 +387,7 @@ extern "C" int t0mi_w4a16_gemm(t0mi_ctx* ctx, uint64_t a, uint64_t qweight, uint
     if (rc) return rc;
     return run_gemm_auto(ctx, T0MI_NN, a, (uint64_t)ctx->cvt, y, m, n, k, out_dtype);
   }
-  if (m > kDecodeMaxRows && (group & (group - 1)) == 0) {
+  if (m > kDecodeMaxRows) {  // power-of-two group here
     // Many rows: dequant fused into the MFMA K-loop, weights read once per tile column.
     W4PrefillParams q;
     memset(&q, 0, sizeof q);

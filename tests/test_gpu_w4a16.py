@@ -81,6 +81,7 @@ def test_w4a16_vs_oracle(rt, m, k, n, group, pgz):
     (767, 256, 136, 128, True),      # last row count of the fused kernel
     (768, 256, 136, 128, True),      # first of the two-pass route (dequant to bf16, dense GEMM)
     (800, 384, 264, 96, True),       # two-pass with a group that is not a power of two
+    (100, 384, 136, 96, True),       # fused range, group not a power of two -> two-pass
     (1024, 1024, 512, 128, True),
     (1100, 384, 520, 128, False),
 ])
