@@ -20,6 +20,12 @@
  *    (m, k, n), GemmTuner::tune takes (m, n, k).
  *  - Grids are HSA work-item grids, as in the reference (grid_x = tiles * wg);
  *    the HIP shim converts them to workgroup counts at launch.
+ *  - Threads: a runtime (t0mi_ctx) may be shared, like the reference's
+ *    Arc<GpuRuntime>.  Its kernel cache and allocation table are locked, and
+ *    every call that launches work or uses the runtime's workspace holds a
+ *    per-runtime lock, so launches reach its stream in call order; waits run
+ *    outside the lock.  A capture (t0mi_capture_begin .. _end) records what
+ *    any thread launches on the runtime meanwhile: capture from one thread.
  */
 #ifndef T0MI_H
 #define T0MI_H

@@ -53,6 +53,10 @@ struct t0mi_ctx {
   std::mutex mu;
   std::map<std::string, std::unique_ptr<t0mi_kernel>> kernels;  // name -> kernel (ensure_kernel_t0 cache)
   std::map<uint64_t, size_t> allocs;                            // live t0mi_alloc buffers
+  // Held by every call that launches work or uses ws / cvt, so a runtime can be
+  // shared between threads (launches reach the stream in lock order).
+  // Recursive: entry points call each other.  Waits run outside it.
+  std::recursive_mutex submit_mu;
   // Library-owned workspace (split-K partial planes, W4A16 partials).
   void* ws = nullptr;
   size_t ws_bytes = 0;
@@ -69,6 +73,9 @@ struct t0mi_ctx {
   std::vector<uint8_t> last_ka;
   int cu_count = 256;
 };
+
+// Scoped hold of ctx->submit_mu (ctx must be non-null).
+#define T0MI_SUBMIT_GUARD(ctx) std::lock_guard<std::recursive_mutex> t0mi_submit_guard_((ctx)->submit_mu)
 
 namespace t0mi {
 // Grows ctx->ws to at least `bytes` (waits for the stream first).

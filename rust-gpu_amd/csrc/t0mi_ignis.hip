@@ -209,6 +209,7 @@ size_t align256(size_t v) { return (v + 255) & ~(size_t)255; }
 extern "C" int t0mi_f32_to_bf16(t0mi_ctx* ctx, uint64_t src_f32, uint64_t dst_bf16, uint64_t count) {
   int rc = check_ctx(ctx);
   if (rc) return rc;
+  T0MI_SUBMIT_GUARD(ctx);
   if (count == 0) return T0MI_OK;
   if (!src_f32 || !dst_bf16) return set_error(T0MI_ERR_INVALID, "null pointer");
   if ((src_f32 & 15) || (dst_bf16 & 15)) return set_error(T0MI_ERR_INVALID, "buffers must be 16-byte aligned");
@@ -224,6 +225,7 @@ extern "C" int t0mi_matmul_f32(t0mi_ctx* ctx, uint64_t x, uint64_t w, uint64_t y
                                uint32_t n) {
   int rc = common_checks(ctx, x, w, y);
   if (rc) return rc;
+  T0MI_SUBMIT_GUARD(ctx);
   if (m == 0 || n == 0) return T0MI_OK;
   const uint32_t kp = up8(k), np = up8(n);
   const size_t xa = align256((size_t)m * kp * 2), wb = align256((size_t)kp * np * 2);
@@ -242,6 +244,7 @@ extern "C" int t0mi_matmul_wt_bf16(t0mi_ctx* ctx, uint64_t x, uint64_t wt_bf16, 
                                    uint32_t k, uint32_t n) {
   int rc = common_checks(ctx, x, wt_bf16, y);
   if (rc) return rc;
+  T0MI_SUBMIT_GUARD(ctx);
   if (k % 8 || n % 8) return set_error(T0MI_ERR_INVALID, "K=%u and N=%u must be multiples of 8 (WT is used in place)", k, n);
   if (wt_bf16 & 15) return set_error(T0MI_ERR_INVALID, "WT must be 16-byte aligned");
   if (m == 0 || n == 0) return T0MI_OK;
@@ -258,6 +261,7 @@ extern "C" int t0mi_matmul_backward_data(t0mi_ctx* ctx, uint64_t dy, uint64_t w,
                                          uint32_t k, uint32_t n) {
   int rc = common_checks(ctx, dy, w, dx);
   if (rc) return rc;
+  T0MI_SUBMIT_GUARD(ctx);
   if (m == 0 || k == 0) return T0MI_OK;
   const uint32_t cp = up8(n), op = up8(k);  // contraction n, output columns k
   const size_t da = align256((size_t)m * cp * 2), wb = align256((size_t)op * cp * 2);
@@ -277,6 +281,7 @@ extern "C" int t0mi_matmul_backward_weight(t0mi_ctx* ctx, uint64_t x, uint64_t d
                                            uint32_t k, uint32_t n) {
   int rc = common_checks(ctx, x, dy, dw);
   if (rc) return rc;
+  T0MI_SUBMIT_GUARD(ctx);
   if (k == 0 || n == 0) return T0MI_OK;
   const uint32_t cp = up8(m), np = up8(n);  // contraction m, output columns n
   const size_t xa = align256((size_t)k * cp * 2), db = align256((size_t)cp * np * 2);
@@ -295,6 +300,7 @@ extern "C" int t0mi_gptq_convert(t0mi_ctx* ctx, uint64_t packed, uint64_t scales
                                  uint64_t scales_bf16, uint64_t qzeros) {
   int rc = check_ctx(ctx);
   if (rc) return rc;
+  T0MI_SUBMIT_GUARD(ctx);
   if (!packed || !scales_f32 || !zeros_i32 || !qweight || !scales_bf16 || !qzeros)
     return set_error(T0MI_ERR_INVALID, "null pointer");
   if (group == 0 || cols % group) return set_error(T0MI_ERR_INVALID, "K=%u must be a multiple of group=%u", cols, group);

@@ -103,6 +103,7 @@ extern "C" int t0mi_capture_begin(t0mi_ctx* ctx) {
   if (rc) return rc;
   if (ctx->null_backend) return set_error(T0MI_ERR_NO_DEVICE, "null runtime has no stream to capture");
   if (!ctx->stream) return set_error(T0MI_ERR_INVALID, "the null (default) stream cannot be captured");
+  T0MI_SUBMIT_GUARD(ctx);
   rc = refuse_if_capturing(ctx, "t0mi_capture_begin");
   if (rc) return rc;
   (void)hipSetDevice(ctx->device);
@@ -115,6 +116,7 @@ extern "C" int t0mi_capture_end(t0mi_ctx* ctx, t0mi_graph** out) {
   if (!ctx || !out) return set_error(T0MI_ERR_INVALID, "null argument");
   *out = nullptr;
   if (ctx->null_backend) return set_error(T0MI_ERR_NO_DEVICE, "null runtime has no stream to capture");
+  T0MI_SUBMIT_GUARD(ctx);
   hipGraph_t g = nullptr;
   hipError_t e = hipStreamEndCapture(ctx->stream, &g);
   if (e != hipSuccess) {
@@ -142,6 +144,7 @@ extern "C" int t0mi_graph_launch(t0mi_graph* g) {
   if (!g) return set_error(T0MI_ERR_INVALID, "null graph");
   int rc = check_ctx(g->ctx);
   if (rc) return rc;
+  T0MI_SUBMIT_GUARD(g->ctx);
   rc = refuse_if_capturing(g->ctx, "t0mi_graph_launch");
   if (rc) return rc;
   hipError_t e = hipGraphLaunch(g->exec, g->ctx->stream);

@@ -342,7 +342,10 @@ extern "C" int t0mi_alloc(t0mi_ctx* ctx, size_t bytes, uint64_t* dptr) {
 extern "C" int t0mi_alloc_zero(t0mi_ctx* ctx, size_t bytes, uint64_t* dptr) {
   int rc = t0mi_alloc(ctx, bytes, dptr);
   if (rc) return rc;
-  rc = fill_async(ctx, (void*)*dptr, 0, bytes);
+  {
+    T0MI_SUBMIT_GUARD(ctx);
+    rc = fill_async(ctx, (void*)*dptr, 0, bytes);
+  }
   if (rc) return rc;
   hipError_t e = hipStreamSynchronize(ctx->stream);
   return e == hipSuccess ? T0MI_OK : hip_fail(e, "hipStreamSynchronize");
@@ -379,6 +382,7 @@ extern "C" int t0mi_d2h(t0mi_ctx* ctx, void* dst, uint64_t src, size_t bytes) {
 extern "C" int t0mi_memset(t0mi_ctx* ctx, uint64_t dst, int value, size_t bytes) {
   if (!ctx || ctx->null_backend) return set_error(T0MI_ERR_INVALID, "no device runtime");
   if (bytes && !dst) return set_error(T0MI_ERR_INVALID, "null destination");
+  T0MI_SUBMIT_GUARD(ctx);
   return fill_async(ctx, (void*)dst, (uint8_t)value, bytes);
 }
 
@@ -554,6 +558,7 @@ static int dispatch_impl(t0mi_ctx* ctx, const t0mi_kernel* k, const uint32_t gri
                          size_t ka_len) {
   int rc = check_ctx(ctx);
   if (rc) return rc;
+  T0MI_SUBMIT_GUARD(ctx);
   if (!k || !grid || (!ka && ka_len)) return set_error(T0MI_ERR_INVALID, "null argument");
   // gpu_context.rs:319-323: builder and kernel declaration must agree.
   if (ka_len != k->kernarg_size)
@@ -688,6 +693,7 @@ extern "C" int t0mi_gemm(t0mi_ctx* ctx, const t0mi_gemm_config* cfg, uint64_t x,
                          uint64_t bias, uint32_t m, uint32_t n, uint32_t k) {
   int rc = check_ctx(ctx);
   if (rc) return rc;
+  T0MI_SUBMIT_GUARD(ctx);
   if (!cfg) return set_error(T0MI_ERR_INVALID, "null config");
   std::string why;
   if (!config_feasible(*cfg, &why))
@@ -750,6 +756,7 @@ extern "C" int t0mi_tile_gemm(t0mi_ctx* ctx, const t0mi_tile_spec* s, uint64_t x
                               float clamp_max) {
   int rc = check_ctx(ctx);
   if (rc) return rc;
+  T0MI_SUBMIT_GUARD(ctx);
   if (!s) return set_error(T0MI_ERR_INVALID, "null spec");
   EpiChain chain;
   std::string why;

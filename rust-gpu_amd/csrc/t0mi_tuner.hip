@@ -304,6 +304,8 @@ extern "C" int t0mi_tuner_tune(t0mi_tuner* t, t0mi_ctx* ctx, uint32_t m, uint32_
   int rc = check_ctx(ctx);
   if (rc) return rc;
   if (ctx->null_backend) return set_error(T0MI_ERR_NO_DEVICE, "tuning needs a device runtime");
+  // Other threads' work on this runtime waits until the timings are done.
+  T0MI_SUBMIT_GUARD(ctx);
   // 3. candidates from the gfx950 cost model
   std::vector<t0mi_gemm_config> cand = rank_candidates(m, n, k, transpose, out_dtype, nullptr);
   if (cand.size() > t->max_candidates) cand.resize(t->max_candidates);

@@ -353,6 +353,7 @@ extern "C" int t0mi_w4a16_gemm(t0mi_ctx* ctx, uint64_t a, uint64_t qweight, uint
                                uint32_t out_dtype) {
   int rc = check_ctx(ctx);
   if (rc) return rc;
+  T0MI_SUBMIT_GUARD(ctx);
   if (!a || !qweight || !scales || !y) return set_error(T0MI_ERR_INVALID, "null pointer");
   if (group == 0 || group % 32) return set_error(T0MI_ERR_INVALID, "group=%u must be a positive multiple of 32", group);
   if (k % group) return set_error(T0MI_ERR_INVALID, "K=%u must be a multiple of group=%u", k, group);
@@ -515,6 +516,7 @@ extern "C" int t0mi_dequant_int4(t0mi_ctx* ctx, uint64_t qweight, uint64_t scale
                                  uint64_t out, uint32_t k, uint32_t n, uint32_t group, uint32_t round_mode) {
   int rc = check_ctx(ctx);
   if (rc) return rc;
+  T0MI_SUBMIT_GUARD(ctx);
   if (!qweight || !scales || !out) return set_error(T0MI_ERR_INVALID, "null pointer");
   if (group == 0 || k % group || k % 8) return set_error(T0MI_ERR_INVALID, "K=%u must be a multiple of group=%u and 8", k, group);
   if (n % 8) return set_error(T0MI_ERR_INVALID, "N=%u must be a multiple of 8", n);

@@ -85,3 +85,72 @@ def test_gemm_empty_contraction(rt, out_bf16):
         assert np.array_equal(got, want)
     for q in (pb, py, pa):
         rt.free(q)
+
+
+def test_shared_runtime_from_threads():
+    """A runtime shared by threads (the reference shares Arc<GpuRuntime>): split-K GEMMs of
+    growing workspace needs and W4A16 decodes, launched concurrently from four threads,
+    give results bit-identical to a single-threaded run (the workspace is replaced only
+    under the runtime's lock, after its stream has drained)."""
+    import threading
+    from gpu_helpers import empty_dev, from_dev, to_dev, torch
+
+    rt = t0mi.Runtime(device=0)
+    g = np.random.default_rng(5)
+    jobs = []
+    for i, (m, n, k, sk) in enumerate([(96, 256, 1024, 4), (200, 512, 2048, 8), (64, 1024, 4096, 16), (130, 136, 512, 2)]):
+        a = (g.standard_normal((m, k)).astype(np.float32).view(np.uint32) >> 16).astype(np.uint16)
+        b = (g.standard_normal((k, n)).astype(np.float32).view(np.uint32) >> 16).astype(np.uint16)
+        cfg = t0mi.preset("gfx950_128x128_k64_w2x2").copy(transpose=t0mi.NN, split_k=sk)
+        da, pa = to_dev(a)
+        db, pb = to_dev(b)
+        dy, py = empty_dev(m * n * 4, fill=0)
+        jobs.append(("gemm", (cfg, pa, pb, py, m, n, k), dy, (m, n), [da, db]))
+    K, N = 4096, 1024
+    aw = (g.standard_normal((16, K)).astype(np.float32).view(np.uint32) >> 16).astype(np.uint16)
+    w = g.integers(0, 2**32, (K // 8, N), dtype=np.uint32)
+    s = np.full((K // 128, N), 0x3C24, np.uint16)
+    daw, paw = to_dev(aw)
+    dw, pw = to_dev(w)
+    ds, ps = to_dev(s)
+    dyw, pyw = empty_dev(16 * N * 4, fill=0)
+    jobs.append(("w4", (paw, pw, ps, 0, 8, pyw, 16, K, N, 128, t0mi.OUT_F32), dyw, (16, N), [daw, dw, ds]))
+    torch().cuda.synchronize()
+
+    def run(job):
+        kind, args = job[0], job[1]
+        if kind == "gemm":
+            rt.gemm(*args)
+        else:
+            rt.w4a16_gemm(*args)
+
+    for job in jobs:  # single-threaded reference
+        run(job)
+    assert rt.wait_idle() == t0mi.OK
+    ref = [from_dev(j[2], np.float32, j[3]) for j in jobs]
+    for j in jobs:
+        j[2].zero_()
+    torch().cuda.synchronize()
+    rt.close()
+    rt = t0mi.Runtime(device=0)  # fresh runtime: the workspace grows while the threads run
+    errors = []
+
+    def worker(order):
+        try:
+            for _ in range(5):
+                for idx in order:
+                    run(jobs[idx])
+        except Exception as e:  # reported below
+            errors.append(repr(e))
+
+    orders = [[0, 1, 2, 3, 4], [3, 2, 1, 0, 4], [2, 4, 0, 3, 1], [4, 1, 3, 2, 0]]
+    threads = [threading.Thread(target=worker, args=(o,)) for o in orders]
+    for t in threads:
+        t.start()
+    for t in threads:
+        t.join()
+    assert not errors, errors
+    assert rt.wait_idle() == t0mi.OK
+    for j, r in zip(jobs, ref):
+        assert np.array_equal(from_dev(j[2], np.float32, j[3]), r), j[0]
+    rt.close()
