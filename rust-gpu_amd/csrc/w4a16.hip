@@ -436,16 +436,17 @@ extern "C" int t0mi_w4a16_gemm(t0mi_ctx* ctx, uint64_t a, uint64_t qweight, uint
     hipError_t e = hipGetLastError();
     return e == hipSuccess ? T0MI_OK : hip_fail(e, "w4a16 prefill launch");
   }
-  // Decode: 64-column strips; groups of 32..256 K run the v2 kernel (16-wave
-  // workgroups of 8 k-blocks per wave), other groups the generic kernel.
+  // Decode: 64-column strips; groups of 32..256 K run the v2 kernel (8-wave
+  // workgroups of 16 k-blocks per wave, issued and computed in chunks of one
+  // group or 4 blocks), other groups the generic kernel.
   const bool v2 = group == 32 || group == 64 || group == 128 || group == 256;
-  constexpr int KBW2 = 8;
+  constexpr int KBW2 = 16;
   constexpr int WAVES = 8, KBW = 16;  // generic kernel
   const uint32_t kb_tot = k / 32;
-  uint32_t nw2 = 16;
+  uint32_t nw2 = 8;
   if (v2) {
     const uint32_t waves_needed = (kb_tot + KBW2 - 1) / KBW2;
-    nw2 = waves_needed <= 4 ? 4 : (waves_needed <= 8 ? 8 : 16);
+    nw2 = waves_needed <= 4 ? 4 : 8;
   }
   const uint32_t per_part = v2 ? nw2 * KBW2 : WAVES * KBW;
   const uint32_t ky = (kb_tot + per_part - 1) / per_part;
@@ -471,9 +472,11 @@ extern "C" int t0mi_w4a16_gemm(t0mi_ctx* ctx, uint64_t a, uint64_t qweight, uint
       const dim3 grid(strips, ky), block(nw2 * 64);
 #define T0MI_W4_V2(NW, G)                                                                                      \
   if (z)                                                                                                       \
-    hipLaunchKernelGGL((w4a16_decode_v2<NW, KBW2, G / 32, true>), grid, block, 0, ctx->stream, p);           \
+    hipLaunchKernelGGL((w4a16_decode_v2<NW, KBW2, G / 32, true, G <= 128 ? 4 : 2>), grid, block, 0,            \
+                       ctx->stream, p);                                                                        \
   else                                                                                                         \
-    hipLaunchKernelGGL((w4a16_decode_v2<NW, KBW2, G / 32, false>), grid, block, 0, ctx->stream, p);
+    hipLaunchKernelGGL((w4a16_decode_v2<NW, KBW2, G / 32, false, G <= 128 ? 4 : 2>), grid, block, 0,           \
+                       ctx->stream, p);
 #define T0MI_W4_V2_G(NW)                                                                                       \
   switch (group) {                                                                                             \
     case 32: T0MI_W4_V2(NW, 32) break;                                                                         \
@@ -483,10 +486,8 @@ extern "C" int t0mi_w4a16_gemm(t0mi_ctx* ctx, uint64_t a, uint64_t qweight, uint
   }
       if (nw2 == 4) {
         T0MI_W4_V2_G(4)
-      } else if (nw2 == 8) {
-        T0MI_W4_V2_G(8)
       } else {
-        T0MI_W4_V2_G(16)
+        T0MI_W4_V2_G(8)
       }
 #undef T0MI_W4_V2_G
 #undef T0MI_W4_V2

@@ -88,10 +88,14 @@ __device__ __forceinline__ float bf16f(uint32_t h) { return __builtin_bit_cast(f
 // read a clamped, valid address.  Lane (c, g) = (lane % 16, lane / 16) loads
 // the 4 words of columns n0 + 4c .. +3 for K sub-row g of each block and
 // activation row c (rows >= M read row 0 and are never stored).
-template <int NW, int KBW, int KBPG, bool ZEROS>
+template <int NW, int KBW, int KBPG, bool ZEROS, int CH = 1>
 __global__ __launch_bounds__(NW * 64) void w4a16_decode_v2(W4Params p) {
   static_assert(KBW % KBPG == 0, "whole groups per wave");
   constexpr int NG = KBW / KBPG;
+  // CH chunks per wave: chunk c's loads are issued, then its blocks computed,
+  // before chunk c+1's loads (CB blocks, whole groups and pairs per chunk).
+  constexpr int CB = KBW / CH;
+  static_assert(KBW % CH == 0 && CB % KBPG == 0 && CB % 2 == 0, "chunks of whole groups and pairs");
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int c = lane & 15, g = lane >> 4;
   const int n0 = blockIdx.x * 64;
@@ -138,34 +142,36 @@ __global__ __launch_bounds__(NW * 64) void w4a16_decode_v2(W4Params p) {
   // FULL: all KBW blocks of the wave exist (every wave but those at the ragged
   // end of K); then nothing is clamped or skipped and no branch separates the
   // loads from their uses.
-  auto body = [&](auto full_c) {
+  auto body = [&](auto full_c, auto chunk_c) {
     constexpr bool FULL = decltype(full_c)::value;
-    u32x4 wv[KBW], at[KBW];
-    u32x2 sv[NG];
-    uint32_t zv[NG];
+    constexpr int B0 = decltype(chunk_c)::value * CB;  // first block of this chunk
+    constexpr int G0 = B0 / KBPG, NGC = CB / KBPG;      // its groups
+    u32x4 wv[CB], at[CB];
+    u32x2 sv[NGC];
+    uint32_t zv[NGC];
     // Activation loads (L2-resident) first, then scales, weights last: loads
     // complete in issue order, so block b's dequant waits only for weight row b.
 #pragma unroll
-    for (int pp = 0; pp < KBW / 2; ++pp) {
+    for (int pp = 0; pp < CB / 2; ++pp) {
 #pragma unroll
       for (int h = 0; h < 2; ++h) {
         int row = 8 * h + ld_r;
         row = row < (int)p.M ? row : 0;
-        int kofs = (kb0 + 2 * pp) * 32 + 8 * ld_x;
+        int kofs = (kb0 + B0 + 2 * pp) * 32 + 8 * ld_x;
         if (!FULL) kofs = kofs + 8 <= (int)p.K ? kofs : 0;
         at[2 * pp + h] = *(const u32x4*)(p.a + (size_t)row * p.K + kofs);
       }
     }
 #pragma unroll
-    for (int q = 0; q < NG; ++q) {
-      int grp = kb0 / KBPG + q;
+    for (int q = 0; q < NGC; ++q) {
+      int grp = kb0 / KBPG + G0 + q;
       if (!FULL) grp = grp < ngroups ? grp : ngroups - 1;
       sv[q] = *(const u32x2*)(p.scales + (size_t)grp * p.N + ncol_c);
       zv[q] = ZEROS ? p.zeros[(size_t)grp * (p.N / 8) + ncol_c / 8] : 0u;  // shifted at use
     }
 #pragma unroll
-    for (int b = 0; b < KBW; ++b) {
-      int kb = kb0 + b;
+    for (int b = 0; b < CB; ++b) {
+      int kb = kb0 + B0 + b;
       if (!FULL) kb = kb < kb_tot ? kb : kb_tot - 1;
       wv[b] = __builtin_nontemporal_load((const u32x4*)(p.w + (size_t)(kb * 4 + g) * p.N + ncol_c));
     }
@@ -174,19 +180,19 @@ __global__ __launch_bounds__(NW * 64) void w4a16_decode_v2(W4Params p) {
     // Activation pieces -> this wave's LDS slice (slot = lane), read back below
     // in the MFMA layout; LDS operations of one wave complete in order.
 #pragma unroll
-    for (int i = 0; i < KBW; ++i)
-      *(__attribute__((address_space(3))) u32x4*)(size_t)(lds_wave + (uint32_t)((i >> 1) * 2048 + st_off[i & 1])) = at[i];
+    for (int i = 0; i < CB; ++i)
+      *(__attribute__((address_space(3))) u32x4*)(size_t)(lds_wave + (uint32_t)(((B0 + i) >> 1) * 2048 + st_off[i & 1])) = at[i];
 #pragma unroll
-    for (int q = 0; q < NG; ++q) {
-      if (!FULL && q * KBPG >= nkb) break;  // wave-uniform: the ragged end of K
+    for (int q = 0; q < NGC; ++q) {
+      if (!FULL && (G0 + q) * KBPG >= nkb) break;  // wave-uniform: the ragged end of K
       f32x4 P[4], S = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int j = 0; j < 4; ++j) P[j] = (f32x4){0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int i = 0; i < KBPG; ++i) {
-        const int b = q * KBPG + i;
+        const int b = q * KBPG + i;  // block within the chunk
         const u32x4 av = *(const __attribute__((address_space(3))) u32x4*)(size_t)(
-            lds_wave + (uint32_t)((b >> 1) * 2048 + rd_off[b & 1]));
+            lds_wave + (uint32_t)(((B0 + b) >> 1) * 2048 + rd_off[b & 1]));
         const bf16x8_t A = perm_act(av);
         S = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A, ones, S, 0, 0, 0);
         P[0] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A, nib_pairs_ao(wv[b].x, mask, magic), P[0], 0, 0, 0);
@@ -208,9 +214,9 @@ __global__ __launch_bounds__(NW * 64) void w4a16_decode_v2(W4Params p) {
     }
   };
   if (nkb == KBW)
-    body(std::integral_constant<bool, true>{});
+    static_for<CH>([&](auto cc) { body(std::integral_constant<bool, true>{}, cc); });
   else
-    body(std::integral_constant<bool, false>{});
+    static_for<CH>([&](auto cc) { body(std::integral_constant<bool, false>{}, cc); });
 
   // Lane (c, g) holds rows 4g + r, columns 4c + j as acc[j][r].  Stage them as
   // red[wave][row][col] so that each of 256 threads sums one row segment of
