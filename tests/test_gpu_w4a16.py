@@ -176,3 +176,32 @@ def test_w4a16_rejects_bad_shapes(rt):
         rt.w4a16_gemm(16, 16, 16, 0, 8, 16, 16, 4000, 128, 128)  # K % group != 0
     with pytest.raises(t0mi.T0miError):
         rt.w4a16_gemm(16, 16, 16, 0, 8, 16, 16, 4096, 128, 48)   # group % 32 != 0
+
+
+def _random_cases(n_cases=40, seed=0x5EED):
+    """Seeded shapes spread over every route of t0mi_w4a16_gemm: decode slabs (1..80
+    rows), the fused kernel (81..767, power-of-two groups, with and without a K split),
+    dequant-once + dense GEMM (768+ rows, or other groups), ragged N and K."""
+    g = np.random.default_rng(seed)
+    groups = [32, 64, 96, 128, 256, 512]
+    out = []
+    for i in range(n_cases):
+        group = int(g.choice(groups))
+        k = group * int(g.integers(1, max(2, 2048 // group) + 1))
+        k = max(k, 32)
+        n = 8 * int(g.integers(1, 160))
+        m = int(g.choice([int(g.integers(1, 81)), int(g.integers(81, 768)), int(g.integers(768, 1100))],
+                         p=[0.45, 0.4, 0.15]))
+        out.append((i, m, k, n, group, bool(g.integers(0, 2)), bool(g.integers(0, 2)), int(g.integers(0, 16))))
+    return out
+
+
+@pytest.mark.parametrize("i,m,k,n,group,pgz,out_bf16,zp", _random_cases())
+def test_w4a16_random_shapes(rt, i, m, k, n, group, pgz, out_bf16, zp):
+    """Every route against the exact-dequant oracle GEMM (the fused and two-pass routes
+    round the weight to bf16 first, well inside the GEMM tolerance)."""
+    a, q, w, s, z = make_case(m, k, n, group, pgz, seed=0x700 + 16 * i)
+    wf = oracle.dequant_qweight_f32(w, s, z, group, zp)
+    ref = oracle.w4a16_gemm(a, w, s, z, group, zp)
+    y = run_w4a16(rt, a, w, s, z, m, k, n, group, zp_const=zp, out_bf16=out_bf16)
+    check(y, ref, a, wf, k, 6e-3)
