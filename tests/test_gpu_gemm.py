@@ -233,3 +233,35 @@ def test_auto_gemm_known_answer(rt):
     y = from_dev(dy, np.float32, (m, n))
     assert y[0, 0] == -6.0
     assert np.array_equal(y, oracle.gemm_bf16(a, b, "nt"))
+
+
+def _random_gemm_cases(n_cases=30, seed=0xC0FFEE):
+    """Seeded ragged shapes (K and N multiples of 8), both layouts and output types; the
+    config is the cost model's choice for the shape, or a forced split-K variant."""
+    g = np.random.default_rng(seed)
+    out = []
+    for i in range(n_cases):
+        m = int(g.integers(1, 700))
+        n = 8 * int(g.integers(1, 90))
+        k = 8 * int(g.integers(1, 300))
+        out.append((i, m, n, k, int(g.integers(0, 2)), bool(g.integers(0, 2)), int(g.choice([0, 0, 2, 4]))))
+    return out
+
+
+@pytest.mark.parametrize("i,m,n,k,layout,out_bf16,sk", _random_gemm_cases())
+def test_random_shapes_auto_selected(rt, i, m, n, k, layout, out_bf16, sk):
+    nn = layout == t0mi.NN
+    a = oracle.normal_bf16((m, k), 0x900 + 2 * i, 0.0, 1.0)
+    b = oracle.normal_bf16((k, n) if nn else (n, k), 0x901 + 2 * i, 0.0, 1.0)
+    cfg = t0mi.auto_select_layout(m, k, n, layout, t0mi.OUT_BF16 if out_bf16 else t0mi.OUT_F32)
+    if sk:
+        cfg = t0mi.preset("gfx950_128x128_k64_w2x2").copy(transpose=layout, split_k=sk)
+    y = run_gemm(rt, cfg, a, b, m, n, k, out_bf16=out_bf16)
+    ref = oracle.gemm_bf16(a, b, "nn" if nn else "nt")
+    if out_bf16:
+        # the GEMM tolerance plus one bf16 rounding step of the output
+        tol = oracle.gemm_tolerance(k, oracle.bf16_to_f32(a), oracle.bf16_to_f32(b))
+        yf = oracle.bf16_to_f32(y)
+        assert np.all(np.abs(yf - ref) <= tol + np.abs(ref) * 2.0**-8), cfg.name()
+    else:
+        _check_tol(y, ref, a, b, k)
