@@ -165,16 +165,32 @@ __global__ __launch_bounds__(256) void t0mi_splitk_reduce(const float* __restric
                                                           EpiChain epi) {
   const size_t plane = (size_t)M * N;
   const size_t nvec = plane / 4;
+  const uint32_t nq = N / 4;  // N % 8 == 0: a vector never straddles rows
   for (size_t v = blockIdx.x * (size_t)blockDim.x + threadIdx.x; v < nvec; v += (size_t)gridDim.x * blockDim.x) {
     const size_t idx = v * 4;
-    const uint32_t m = (uint32_t)(idx / N), n = (uint32_t)(idx % N);
-    f32x4 s = *(const f32x4*)(ws + idx);
-    for (uint32_t q = 1; q < sk; ++q) {
-      const f32x4 t = *(const f32x4*)(ws + q * plane + idx);
-      s.x += t.x;
-      s.y += t.y;
-      s.z += t.z;
-      s.w += t.w;
+    const uint32_t m = (uint32_t)(v / nq), n = (uint32_t)(v % nq) * 4;
+    // Planes are read four at a time (independent loads in flight together)
+    // and summed in plane order, so the result does not depend on timing.
+    f32x4 s = {0.f, 0.f, 0.f, 0.f};
+    for (uint32_t q0 = 0; q0 < sk; q0 += 4) {
+      f32x4 t[4];
+#pragma unroll
+      for (uint32_t j = 0; j < 4; ++j) {
+        const uint32_t q = q0 + j < sk ? q0 + j : q0;  // past the last plane: a repeat, not added
+        t[j] = *(const f32x4*)(ws + q * plane + idx);
+      }
+#pragma unroll
+      for (uint32_t j = 0; j < 4; ++j) {
+        if (q0 + j >= sk) break;
+        if (q0 + j == 0) {
+          s = t[0];
+        } else {
+          s.x += t[j].x;
+          s.y += t[j].y;
+          s.z += t[j].z;
+          s.w += t[j].w;
+        }
+      }
     }
     if (epi.n) {
       f32x4 bv = {0.f, 0.f, 0.f, 0.f};
