@@ -14,13 +14,16 @@
 // with the activation operand permuted into the same k order as the pairs.
 //
 // Memory plan (HBM-bound: 0.5 B per weight): a workgroup owns a 64-column
-// strip; each of its NW waves owns KBW consecutive 32-K blocks and issues all
-// of its 16-byte weight loads (non-temporal, one 1 KB row segment per
-// instruction), activation loads and scale/zero loads before any compute, so a
-// CU keeps NW * KBW KB of weights in flight; blocks are then dequantized and
-// multiplied in arrival order.  The waves' [16 x 64] fp32 partials are summed
-// through LDS in wave order (deterministic) and stored as 8-byte bf16 (16-byte
-// f32) row segments.
+// strip; each of its NW waves owns KBW consecutive 32-K blocks, taken in CH
+// chunks: a chunk's activation, scale/zero and 16-byte weight loads
+// (non-temporal, one 1 KB row segment per instruction) are issued, then its
+// blocks are dequantized and multiplied in arrival order while later chunks'
+// loads of the other waves are in flight.  A CU accepts load instructions far
+// more slowly than its waves can issue them and serves the oldest waves first;
+// chunking keeps every wave's compute close behind its own data instead of
+// leaving the youngest waves all their work at the end.  The waves' [16 x 64]
+// fp32 partials are summed through LDS in wave order (deterministic) and stored
+// as 8-byte bf16 (16-byte f32) row segments.
 #pragma once
 #include "gemm_bf16_kernel.h"
 
