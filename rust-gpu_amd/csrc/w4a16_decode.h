@@ -221,12 +221,16 @@ __global__ __launch_bounds__(NW * 64) void w4a16_decode_v2(W4Params p) {
   else
     static_for<CH>([&](auto cc) { body(std::integral_constant<bool, false>{}, cc); });
 
-  // Lane (c, g) holds rows 4g + r, columns 4c + j as acc[j][r].  Stage them as
-  // red[wave][row][col] so that each of 256 threads sums one row segment of
-  // 4 columns over the waves (in wave order) and stores it with one vector store.
-  __syncthreads();  // every wave is done with its activation slice
+  // Lane (c, g) holds rows 4g + r, columns 4c + j as acc[j][r].  Each wave
+  // stages its [16 x 64] partial (row-major) at the start of its own
+  // activation slice — its reads of the slice precede these writes in program
+  // order and a wave's LDS operations complete in order — so one barrier
+  // separates the writes from the sum, in which each of 256 threads adds one
+  // row segment of 4 columns over the waves (in wave order) and stores it with
+  // one vector store.
+  static_assert(SMEM_KB * 256 >= 16 * 64, "a wave's slice holds its [16 x 64] partial");
   float* red = smem;
-  float* mine = red + wave * 16 * 64;
+  float* mine = red + wave * SMEM_KB * 256;
 #pragma unroll
   for (int r = 0; r < 4; ++r)
     *(f32x4*)(mine + (4 * g + r) * 64 + 4 * c) = (f32x4){acc[0][r], acc[1][r], acc[2][r], acc[3][r]};
@@ -236,7 +240,7 @@ __global__ __launch_bounds__(NW * 64) void w4a16_decode_v2(W4Params p) {
     f32x4 s4 = *(const f32x4*)(red + R * 64 + 4 * C);
 #pragma unroll
     for (int v = 1; v < NW; ++v) {
-      const f32x4 t4 = *(const f32x4*)(red + (v * 16 + R) * 64 + 4 * C);
+      const f32x4 t4 = *(const f32x4*)(red + v * SMEM_KB * 256 + R * 64 + 4 * C);
       s4.x += t4.x;
       s4.y += t4.y;
       s4.z += t4.z;
