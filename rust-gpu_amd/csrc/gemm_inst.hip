@@ -1,6 +1,7 @@
 // gemm_inst.hip — instantiates one block of gemm_variants.def for one B layout.
 // Compiled six times by the build (T0MI_PART = 0/1/2, T0MI_INST_NN = 0/1, with
 // T0MI_TABLE_FN naming the table accessor) so the variants build in parallel.
+#include "gemm_pingpong.h"
 #include "t0mi_ctx.h"
 
 #ifndef T0MI_PART
@@ -12,10 +13,22 @@
 
 namespace t0mi {
 
+// The NN 256x256x64 2x4-wave configuration runs the ping-pong kernel (same
+// results, bit for bit) whenever its K-granularity precondition holds.
+template <int BM, int BN, int BK, int WM, int WN, int S, bool NN>
+static void launch_variant(dim3 g, hipStream_t s, const GemmParams& p) {
+  if constexpr (NN && BM == 256 && BN == 256 && BK == 64 && WM == 2 && WN == 4 && S == 2) {
+    if (pingpong_ok(p)) {
+      hipLaunchKernelGGL(gemm_bf16_pingpong_kernel<0>, g, dim3(512), 0, s, p);
+      return;
+    }
+  }
+  hipLaunchKernelGGL((gemm_bf16_kernel<BM, BN, BK, WM, WN, S, NN>), g, dim3(WM * WN * 64), 0, s, p);
+}
+
 #define T0MI_V(BM, BN, BK, WM, WN, S)                                                                  \
   static void launch_##BM##_##BN##_##BK##_##WM##_##WN##_##S(dim3 g, hipStream_t s, const GemmParams& p) { \
-    hipLaunchKernelGGL((gemm_bf16_kernel<BM, BN, BK, WM, WN, S, (T0MI_INST_NN != 0)>), g, dim3(WM * WN * 64), 0, s, \
-                       p);                                                                             \
+    launch_variant<BM, BN, BK, WM, WN, S, (T0MI_INST_NN != 0)>(g, s, p);                              \
   }
 #if T0MI_INST_NN
 #define T0MI_V_NT(BM, BN, BK, WM, WN, S)

@@ -1,0 +1,318 @@
+// gemm_pingpong.h — gfx950 bf16 GEMM, NN layout, 256x256x64 tiles, 8 waves in
+// two groups that alternate between LDS reads and MFMA bursts ("ping-pong").
+//
+// Same math and the same per-accumulator MFMA order as gemm_bf16_kernel
+// <256, 256, 64, 2, 4, 2, NN> (so results are bit-identical to it); it replaces
+// that instantiation where its preconditions hold (pingpong_ok below):
+//   src/t0/gemm_gen.rs:668-1438 (generate_lds_db), NN as in BASELINE.json.
+//
+// Schedule.  Waves 0-3 (group 0) own rows 0-127 of the tile and waves 4-7
+// (group 1) rows 128-255; wave w and wave w+4 run on the same SIMD.  Every
+// wave runs, per 64-K tile u, a read phase R(u) (all 32 fragments of the tile
+// from LDS into registers) and an MFMA phase M(u) (the tile's 32 MFMAs, back
+// to back), separated by workgroup barriers.  Group 1 starts one barrier
+// later, so in every barrier interval one wave of each SIMD issues MFMAs while
+// its partner reads LDS: the MFMA pipe is fed by one wave at a time without
+// gaps.  With both waves of a SIMD interleaving reads and MFMAs (the generic
+// kernel) the older wave finishes its tile early and waits at the barrier
+// while the younger one runs alone and cannot keep the pipe busy.
+//
+// LDS (160 KB): B tile ring of 3 slots (32 KB each) and, per group, a ring of
+// 2 slots for its own half of the A tile (16 KB each; each group reads only its
+// own rows).  All global -> LDS DMA is issued inside the MFMA phases (read
+// phases are pure LDS reads):
+//   group 0, M(u): A rows 0-127 of tile u+2 and B k-rows 0-31 of tile u+2;
+//   group 1, M(u): A rows 128-255 of tile u+2 and B k-rows 32-63 of tile u+2.
+// The slot each DMA overwrites was last read one interval earlier, and each
+// wave waits for its DMA (vmcnt 0) at the end of its next read phase, one
+// barrier before the first wave reads it.
+//
+// Ragged edges: A is read through a buffer resource whose record count ends at
+// row M, so rows past M load as zeros; B columns past N are clamped (their
+// products land in columns that are not stored).  K (per split-K partition)
+// must be a multiple of 64 — pingpong_ok() checks it on the host.
+//
+// Output: full tiles with bf16 output are staged through LDS (each wave's
+// 128 x 64 block, 16-byte chunks XOR-swizzled by row) and written as whole
+// 128-byte rows, 8 rows per store instruction; partial tiles, f32 output and
+// split-K partial planes use store_block.
+#pragma once
+#include "gemm_bf16_kernel.h"
+
+namespace t0mi {
+
+// 16-byte buffer -> LDS DMA with range checking: lane i's 16 bytes at
+// rsrc.base + soff + voff land at LDS byte address m0 + 16*i; lanes whose
+// offset is at or beyond the record count write zeros.  Same tracking rules as
+// lds_dma16.
+__device__ __forceinline__ void lds_dma16_rsrc(u32x4 rsrc, uint32_t voff, uint32_t soff, uint32_t lds_byte_addr) {
+  const uint32_t m0v = __builtin_amdgcn_readfirstlane(lds_byte_addr);
+  uint32_t saved;
+  asm volatile(
+      "s_mov_b32 %0, m0\n\t"
+      "s_mov_b32 m0, %4\n\t"
+      "buffer_load_dwordx4 %1, %2, %3 offen lds\n\t"
+      "s_mov_b32 m0, %0"
+      : "=&s"(saved)
+      : "v"(voff), "s"(rsrc), "s"(soff), "s"(m0v)
+      :);
+}
+
+// 16-byte global -> LDS DMA, address = uniform base (SGPR pair) + 32-bit lane offset.
+__device__ __forceinline__ void lds_dma16_sv(const void* sbase, uint32_t voff, uint32_t lds_byte_addr) {
+  const uint32_t m0v = __builtin_amdgcn_readfirstlane(lds_byte_addr);
+  uint32_t saved;
+  asm volatile(
+      "s_mov_b32 %0, m0\n\t"
+      "s_mov_b32 m0, %3\n\t"
+      "global_load_lds_dwordx4 %1, %2\n\t"
+      "s_mov_b32 m0, %0"
+      : "=&s"(saved)
+      : "v"(voff), "s"(sbase), "s"(m0v)
+      :);
+}
+
+// Raw buffer resource: 48-bit base, record count in bytes, gfx9 default flags.
+__device__ __forceinline__ u32x4 make_rsrc(const void* base, uint32_t nbytes) {
+  const uint64_t b = (uint64_t)base;
+  u32x4 r;
+  r.x = __builtin_amdgcn_readfirstlane((uint32_t)b);
+  r.y = __builtin_amdgcn_readfirstlane((uint32_t)(b >> 32) & 0xffffu);
+  r.z = __builtin_amdgcn_readfirstlane(nbytes);
+  r.w = __builtin_amdgcn_readfirstlane(0x00020000u);
+  return r;
+}
+
+// Host-side check of the ping-pong kernel's preconditions (the NN 256x256x64
+// 2x4-wave configuration is assumed by the caller).
+inline bool pingpong_ok(const GemmParams& p) {
+  if (p.K == 0 || p.K % 64 != 0) return false;
+  if (p.split_k > 1 && p.k_per_split % 64 != 0) return false;
+  if (p.N < 8) return false;
+  return true;
+}
+
+// (A template only so that every translation unit may include the definition.)
+template <int UNUSED = 0>
+__global__ __launch_bounds__(512) void gemm_bf16_pingpong_kernel(GemmParams p) {
+  constexpr int BK = 64, BN = 256, TN = 64;
+  constexpr int FM = 4, FN = 2, KC = 8, KS = 4, NC = 32;
+  constexpr int B_ELEMS = BN * BK, AH_ELEMS = 128 * BK;  // B tile, half A tile
+  constexpr int NR = FM + 2 * FN;                         // LDS reads per k-step
+  __shared__ __attribute__((aligned(1024))) uint16_t smem[3 * B_ELEMS + 4 * AH_ELEMS];
+
+  int tm, tn, part;
+  tile_coords(p, tm, tn, part);
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+  const int g = wave >> 2, w4 = wave & 3;  // group, wave within the group
+  const bool g0 = g == 0;
+  const int wn = wave & 3;                 // 64-column slice of the tile
+  const int m0 = tm * 256, n0 = tn * BN;
+  const int kbeg = part * (int)p.k_per_split;
+  int kend = kbeg + (int)p.k_per_split;
+  if (kend > (int)p.K) kend = (int)p.K;
+  const int nk = kend > kbeg ? (kend - kbeg) / BK : 0;
+  const uint32_t smem_base = lds_addr(smem);
+  const uint32_t a_slot0 = smem_base + (uint32_t)(3 * B_ELEMS * 2 + g * 2 * AH_ELEMS * 2);
+
+  // ---- DMA addressing ------------------------------------------------------
+  // Wave w4 of group g fills, per tile, 1 KB blocks w4 + 4j (j = 0..3) of its
+  // half of the A tile (8 rows x 64 K each) and blocks 16g + w4 + 4j of the B
+  // tile (2 k-rows x 256 columns each).  The swizzles depend on the row modulo
+  // 32 (A) and 4 (B) only, which j does not change, so one lane offset serves
+  // all four loads of a kind; j and the tile move the uniform base.
+  uint32_t a_voff, b_voff;
+  {
+    const int row = w4 * 8 + (lane >> 3), pc = lane & 7;
+    a_voff = (uint32_t)(row * (int)p.lda + ((pc ^ swz<KC>(row)) * 8)) * 2u;
+    const int brow = 2 * (16 * g + w4) + (lane >> 5), bpc = lane & 31;
+    int gn = n0 + ((bpc ^ swz_nn<NC>(brow)) * 8);
+    gn = gn < (int)p.N ? gn : (int)p.N - 8;
+    b_voff = (uint32_t)(brow * (int)p.ldb + gn) * 2u;
+  }
+  // A through four buffer resources, one per 32-row block j of this group's
+  // half, fixed for the whole K loop: base = row block start, record count =
+  // bytes up to the end of row M-1 (0 for blocks past M), so lanes on rows >= M
+  // read zeros.  The tile's K position goes in the scalar offset operand; valid
+  // rows stay in range and rows past M out of range whether or not the range
+  // check counts that operand (k0 + 64 <= K <= lda).
+  const uint64_t a_row_bytes = (uint64_t)p.lda * 2u;
+  u32x4 a_rs[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int rows = (int)p.M - (m0 + g * 128 + j * 32);
+    const uint64_t left = rows <= 0 ? 0u : (uint64_t)rows * a_row_bytes;
+    // The base is not dereferenced when the record count is 0.
+    a_rs[j] = make_rsrc((const char*)p.a + (uint64_t)(m0 + g * 128 + j * 32) * a_row_bytes,
+                        left > 0x7fffffffu ? 0x7fffffffu : (uint32_t)left);
+  }
+  const uint64_t b_row_bytes = (uint64_t)p.ldb * 2u;
+  const uint32_t b_lds0 = smem_base + (16 * g + w4) * 1024;
+  const uint32_t a_lds0 = a_slot0 + w4 * 1024;
+  // DMA j of tile t: j < 4 from A row block j, else B k-rows 8(j-4) .. +1 of the
+  // wave's B block (the tile's base address is formed once per phase).
+  auto dma = [&](int t, const char* b_tile, auto jc) {
+    constexpr int j = decltype(jc)::value;
+    if constexpr (j < 4) {
+      lds_dma16_rsrc(a_rs[j], a_voff, (uint32_t)(kbeg + t * BK) * 2u,
+                     a_lds0 + (uint32_t)((t & 1) * AH_ELEMS * 2) + 4 * j * 1024);
+    } else {
+      lds_dma16_sv(b_tile + (uint64_t)(j - 4) * 8u * b_row_bytes, b_voff,
+                   b_lds0 + (uint32_t)((t % 3) * B_ELEMS * 2) + 4 * (j - 4) * 1024);
+    }
+  };
+  auto b_tile_of = [&](int t) { return (const char*)p.b + (uint64_t)(kbeg + t * BK) * b_row_bytes; };
+
+  // ---- LDS -> fragments (same addressing as gemm_bf16_kernel, NN) -----------
+  const int lrow = lane & 31, lhalf = lane >> 5;
+  int a_off[KS];
+#pragma unroll
+  for (int ks = 0; ks < KS; ++ks) a_off[ks] = lrow * BK + (((ks * 2 + lhalf) ^ swz<KC>(lrow)) * 8);
+  const int tg = lane >> 4, ti = lane & 15;
+  const int nn_krow0 = 8 * (tg >> 1) + (ti >> 2);
+  const int nn_col0 = wn * TN + 16 * (tg & 1) + 4 * (ti & 3);
+  const int nn_sw = swz_nn<NC>(nn_krow0);
+
+  bf16x8 xa[KS][FM], xb[KS][FN];
+  i16x4 tr[KS][FN][2];
+  auto read_one = [&](const uint16_t* As, const uint16_t* Bs, auto ic) {
+    constexpr int i = decltype(ic)::value;
+    constexpr int ks = i / NR, r = i % NR;
+    if constexpr (r < FM) {
+      xa[ks][r] = *(const bf16x8*)(As + a_off[ks] + r * 32 * BK);
+    } else {
+      constexpr int fn = (r - FM) / 2, h = (r - FM) % 2;
+      const int col = nn_col0 + fn * 32;
+      const int eoff = (((col >> 3) ^ nn_sw) << 3) + (col & 4);
+      const int krow = ks * 16 + 4 * h + nn_krow0;
+      tr[ks][fn][h] = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+          (__attribute__((address_space(3))) i16x4*)(Bs + krow * BN + eoff));
+      if constexpr (h == 1)
+        xb[ks][fn] = __builtin_bit_cast(bf16x8, __builtin_shufflevector(tr[ks][fn][0], tr[ks][fn][1], 0, 1, 2, 3,
+                                                                        4, 5, 6, 7));
+    }
+  };
+
+  f32x16 acc[FN][FM];
+#pragma unroll
+  for (int fn = 0; fn < FN; ++fn)
+#pragma unroll
+    for (int fm = 0; fm < FM; ++fm)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[fn][fm][r] = 0.0f;
+
+  const uint16_t* a_slots = smem + 3 * B_ELEMS + g * 2 * AH_ELEMS;
+  auto read_phase = [&](int u) {
+    const uint16_t* As = a_slots + (u & 1) * AH_ELEMS;
+    const uint16_t* Bs = smem + (u % 3) * B_ELEMS;
+    static_for<KS * NR>([&](auto ic) {
+      read_one(As, Bs, ic);
+      __builtin_amdgcn_sched_barrier(0);
+    });
+    wait_lgkmcnt0();
+  };
+  // The tile's MFMAs in k-step order (the generic kernel's accumulation order);
+  // with DMA, load j of tile td follows MFMA 16 + 2j.
+  auto mfma_phase = [&](auto dma_c, int td) {
+    constexpr bool D = decltype(dma_c)::value;
+    const char* b_td = D ? b_tile_of(td) : nullptr;
+    static_for<KS * FN * FM>([&](auto ic) {
+      constexpr int i = decltype(ic)::value;
+      constexpr int ks = i / (FN * FM), fn = (i / FM) % FN, fm = i % FM;
+      acc[fn][fm] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(xb[ks][fn], xa[ks][fm], acc[fn][fm], 0, 0, 0);
+      if constexpr (D && i >= 16 && (i - 16) % 2 == 0) dma(td, b_td, std::integral_constant<int, (i - 16) / 2>{});
+      __builtin_amdgcn_sched_barrier(0);
+    });
+  };
+  auto bar = []() {
+    __builtin_amdgcn_sched_barrier(0);
+    __syncthreads();
+    __builtin_amdgcn_sched_barrier(0);
+  };
+  using True = std::integral_constant<bool, true>;
+  using False = std::integral_constant<bool, false>;
+
+  // Every wave runs R(u) bar M(u) bar; group 1 starts one barrier later and
+  // group 0 ends with one extra, so both pass 2*nk + 1 barriers.
+  if (nk > 0) static_for<8>([&](auto jc) { dma(0, b_tile_of(0), jc); });
+  if (nk > 1) static_for<8>([&](auto jc) { dma(1, b_tile_of(1), jc); });
+  wait_vmcnt<0>();
+  bar();
+  if (!g0) bar();
+  int u = 0;
+  for (; u + 2 < nk; ++u) {
+    read_phase(u);
+    wait_vmcnt<0>();  // this wave's DMA of tile u+1 (issued in M(u-1)) landed
+    bar();
+    mfma_phase(True{}, u + 2);
+    bar();
+  }
+  for (; u < nk; ++u) {
+    read_phase(u);
+    wait_vmcnt<0>();
+    bar();
+    mfma_phase(False{}, 0);
+    if (u + 1 < nk) bar();
+  }
+  if (g0) bar();
+  // Here every wave has finished its LDS reads and DMA (group 0 met group 1
+  // at the barrier after group 1's last read phase).
+
+  // ---- epilogue ------------------------------------------------------------
+  const bool partial_plane = p.split_k > 1;
+  char* ybase = (char*)p.y + (partial_plane ? (size_t)part * p.y_split_stride : 0);
+  const int row0 = m0 + g * 128;
+  const int col0 = n0 + wn * TN;
+  if (!partial_plane && p.out_bf16 && m0 + 256 <= (int)p.M && n0 + 256 <= (int)p.N) {
+    char* st = (char*)smem + wave * 16384;  // this wave's 128 x 64 bf16 block
+    static_for<FM>([&](auto fmc) {
+      constexpr int fm = decltype(fmc)::value;
+      static_for<FN>([&](auto fnc) {
+        constexpr int fn = decltype(fnc)::value;
+        const int r = fm * 32 + lrow;
+#pragma unroll
+        for (int gq = 0; gq < 4; ++gq) {
+          float v0 = acc[fn][fm][gq * 4 + 0], v1 = acc[fn][fm][gq * 4 + 1];
+          float v2 = acc[fn][fm][gq * 4 + 2], v3 = acc[fn][fm][gq * 4 + 3];
+          if (p.epi.n) {
+            const int nc = col0 + fn * 32 + gq * 8 + lhalf * 4;
+            f32x4 bv = {0.0f, 0.0f, 0.0f, 0.0f};
+            if (p.bias) bv = f32x4{p.bias[nc], p.bias[nc + 1], p.bias[nc + 2], p.bias[nc + 3]};
+            v0 = epi_apply(v0, bv.x, p.epi);
+            v1 = epi_apply(v1, bv.y, p.epi);
+            v2 = epi_apply(v2, bv.z, p.epi);
+            v3 = epi_apply(v3, bv.w, p.epi);
+          }
+          const int c = fn * 4 + gq;  // 16-byte chunk of the 128-byte row
+          u32x2 o;
+          o.x = pack_bf16x2(v0, v1);
+          o.y = pack_bf16x2(v2, v3);
+          *(u32x2*)(st + r * 128 + ((c ^ (r & 7)) * 16) + lhalf * 8) = o;
+        }
+      });
+    });
+    wait_lgkmcnt0();  // the block is only read back by the wave that wrote it
+    const int rr = lane >> 3, cc = lane & 7;
+    char* yrow = ybase + ((size_t)(row0 + rr) * p.ldy + col0 + cc * 8) * 2;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const int r = i * 8 + rr;
+      const u32x4 v = *(const u32x4*)(st + r * 128 + ((cc ^ (r & 7)) * 16));
+      *(u32x4*)(yrow + (size_t)i * 8 * p.ldy * 2) = v;
+    }
+  } else {
+    static_for<FM>([&](auto fmc) {
+      constexpr int fm = decltype(fmc)::value;
+      const int m = row0 + fm * 32 + lrow;
+      if (m < (int)p.M) {
+        static_for<FN>([&](auto fnc) {
+          constexpr int fn = decltype(fnc)::value;
+          store_block(p, acc[fn][fm], ybase, m, col0 + fn * 32 + lhalf * 4, partial_plane);
+        });
+      }
+    });
+  }
+}
+
+}  // namespace t0mi
