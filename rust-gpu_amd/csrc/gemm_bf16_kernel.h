@@ -221,6 +221,57 @@ __device__ __forceinline__ void wait_lgkmcnt0() { __builtin_amdgcn_s_waitcnt(0xF
 // same number of DMA loads (the vmcnt arithmetic below relies on it).
 static __device__ __attribute__((aligned(16))) const uint32_t g_zero16[4] = {0u, 0u, 0u, 0u};
 
+// Stores a wave's FM*32 x FN*32 accumulator block as bf16 through a private
+// LDS block `st` (FM*32 * FN*32 * 2 bytes): each lane writes its 8-byte row
+// pieces with the 16-byte chunks of every row XOR-swizzled by the row index,
+// then the block is read back so that each 16-byte-per-lane store instruction
+// writes 512 / (FN*32) whole rows of FN*64 contiguous bytes (the direct stores
+// of store_block write 16 bytes into each of 32 rows).  The epilogue chain is
+// applied before the conversion.  Caller's contract: a full tile (all rows and
+// columns in range), bf16 output, not a partial plane, 16-byte aligned Y, and
+// no pending LDS reads or DMA into `st`.
+template <int FM, int FN>
+__device__ __forceinline__ void store_tile_bf16_staged(const GemmParams& p, const f32x16 (&acc)[FN][FM], char* st,
+                                                       char* ybase, int row0, int col0, int lane) {
+  constexpr int TN = FN * 32, CH = TN / 8, RPI = 64 / CH;  // 16-byte chunks per row, rows per store
+  const int lrow = lane & 31, lhalf = lane >> 5;
+  static_for<FM>([&](auto fmc) {
+    constexpr int fm = decltype(fmc)::value;
+    static_for<FN>([&](auto fnc) {
+      constexpr int fn = decltype(fnc)::value;
+      const int r = fm * 32 + lrow;
+#pragma unroll
+      for (int gq = 0; gq < 4; ++gq) {
+        float v0 = acc[fn][fm][gq * 4 + 0], v1 = acc[fn][fm][gq * 4 + 1];
+        float v2 = acc[fn][fm][gq * 4 + 2], v3 = acc[fn][fm][gq * 4 + 3];
+        if (p.epi.n) {
+          const int nc = col0 + fn * 32 + gq * 8 + lhalf * 4;
+          f32x4 bv = {0.0f, 0.0f, 0.0f, 0.0f};
+          if (p.bias) bv = f32x4{p.bias[nc], p.bias[nc + 1], p.bias[nc + 2], p.bias[nc + 3]};
+          v0 = epi_apply(v0, bv.x, p.epi);
+          v1 = epi_apply(v1, bv.y, p.epi);
+          v2 = epi_apply(v2, bv.z, p.epi);
+          v3 = epi_apply(v3, bv.w, p.epi);
+        }
+        const int c = fn * 4 + gq;  // 16-byte chunk of the row
+        u32x2 o;
+        o.x = pack_bf16x2(v0, v1);
+        o.y = pack_bf16x2(v2, v3);
+        *(u32x2*)(st + r * TN * 2 + ((c ^ (r & (CH - 1))) * 16) + lhalf * 8) = o;
+      }
+    });
+  });
+  wait_lgkmcnt0();  // the block is read back only by the wave that wrote it
+  const int rr = lane / CH, cc = lane % CH;
+  char* yrow = ybase + ((size_t)(row0 + rr) * p.ldy + col0 + cc * 8) * 2;
+#pragma unroll
+  for (int i = 0; i < FM * 32 / RPI; ++i) {
+    const int r = i * RPI + rr;
+    const u32x4 v = *(const u32x4*)(st + r * TN * 2 + ((cc ^ (r & (CH - 1))) * 16));
+    *(u32x4*)(yrow + (size_t)i * RPI * p.ldy * 2) = v;
+  }
+}
+
 template <int BM, int BN, int BK, int WM, int WN, int S, bool NN>
 struct GemmTile {
   static constexpr int NWAVES = WM * WN;
@@ -553,6 +604,16 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_bf16_kernel(GemmParams p) {
   // acc is only ever indexed by constants and stays in registers.
   const bool partial_plane = p.split_k > 1;
   char* ybase = (char*)p.y + (partial_plane ? (size_t)part * p.y_split_stride : 0);
+  // Full tiles with bf16 output: stage each wave's block through the (now
+  // idle) LDS ring and store whole rows, when the blocks fit in it.
+  if constexpr (BM * BN <= S * BUF) {
+    if (!partial_plane && p.out_bf16 && m0 + BM <= (int)p.M && n0 + BN <= (int)p.N && ((uintptr_t)p.y & 15) == 0) {
+      __syncthreads();  // every wave has read its last fragments (no DMA is pending)
+      store_tile_bf16_staged<FM, FN>(p, acc, (char*)smem + wave * TM * TN * 2, ybase, m0 + wm * TM,
+                                     n0 + wn * TN, lane);
+      return;
+    }
+  }
   static_for<FM>([&](auto fmc) {
     constexpr int fm = decltype(fmc)::value;
     const int m = m0 + wm * TM + fm * 32 + lrow;

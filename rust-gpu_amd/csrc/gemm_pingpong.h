@@ -32,9 +32,9 @@
 // products land in columns that are not stored).  K (per split-K partition)
 // must be a multiple of 64 — pingpong_ok() checks it on the host.
 //
-// Output: full tiles with bf16 output are staged through LDS (each wave's
-// 128 x 64 block, 16-byte chunks XOR-swizzled by row) and written as whole
-// 128-byte rows, 8 rows per store instruction; partial tiles, f32 output and
+// Output: full tiles with bf16 output (16-byte aligned Y) are staged through
+// LDS by store_tile_bf16_staged (each wave's 128 x 64 block, written as whole
+// 128-byte rows, 8 rows per store instruction); partial tiles, f32 output and
 // split-K partial planes use store_block.
 #pragma once
 #include "gemm_bf16_kernel.h"
@@ -264,43 +264,8 @@ __global__ __launch_bounds__(512) void gemm_bf16_pingpong_kernel(GemmParams p) {
   char* ybase = (char*)p.y + (partial_plane ? (size_t)part * p.y_split_stride : 0);
   const int row0 = m0 + g * 128;
   const int col0 = n0 + wn * TN;
-  if (!partial_plane && p.out_bf16 && m0 + 256 <= (int)p.M && n0 + 256 <= (int)p.N) {
-    char* st = (char*)smem + wave * 16384;  // this wave's 128 x 64 bf16 block
-    static_for<FM>([&](auto fmc) {
-      constexpr int fm = decltype(fmc)::value;
-      static_for<FN>([&](auto fnc) {
-        constexpr int fn = decltype(fnc)::value;
-        const int r = fm * 32 + lrow;
-#pragma unroll
-        for (int gq = 0; gq < 4; ++gq) {
-          float v0 = acc[fn][fm][gq * 4 + 0], v1 = acc[fn][fm][gq * 4 + 1];
-          float v2 = acc[fn][fm][gq * 4 + 2], v3 = acc[fn][fm][gq * 4 + 3];
-          if (p.epi.n) {
-            const int nc = col0 + fn * 32 + gq * 8 + lhalf * 4;
-            f32x4 bv = {0.0f, 0.0f, 0.0f, 0.0f};
-            if (p.bias) bv = f32x4{p.bias[nc], p.bias[nc + 1], p.bias[nc + 2], p.bias[nc + 3]};
-            v0 = epi_apply(v0, bv.x, p.epi);
-            v1 = epi_apply(v1, bv.y, p.epi);
-            v2 = epi_apply(v2, bv.z, p.epi);
-            v3 = epi_apply(v3, bv.w, p.epi);
-          }
-          const int c = fn * 4 + gq;  // 16-byte chunk of the 128-byte row
-          u32x2 o;
-          o.x = pack_bf16x2(v0, v1);
-          o.y = pack_bf16x2(v2, v3);
-          *(u32x2*)(st + r * 128 + ((c ^ (r & 7)) * 16) + lhalf * 8) = o;
-        }
-      });
-    });
-    wait_lgkmcnt0();  // the block is only read back by the wave that wrote it
-    const int rr = lane >> 3, cc = lane & 7;
-    char* yrow = ybase + ((size_t)(row0 + rr) * p.ldy + col0 + cc * 8) * 2;
-#pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      const int r = i * 8 + rr;
-      const u32x4 v = *(const u32x4*)(st + r * 128 + ((cc ^ (r & 7)) * 16));
-      *(u32x4*)(yrow + (size_t)i * 8 * p.ldy * 2) = v;
-    }
+  if (!partial_plane && p.out_bf16 && m0 + 256 <= (int)p.M && n0 + 256 <= (int)p.N && ((uintptr_t)p.y & 15) == 0) {
+    store_tile_bf16_staged<FM, FN>(p, acc, (char*)smem + wave * 16384, ybase, row0, col0, lane);
   } else {
     static_for<FM>([&](auto fmc) {
       constexpr int fm = decltype(fmc)::value;

@@ -73,6 +73,19 @@ def test_integer_pattern_exact_all_variants(rt, name, layout):
 
 
 @pytest.mark.parametrize("layout", [t0mi.NT, t0mi.NN])
+@pytest.mark.parametrize("name", [v[0] for v in ALL_VARIANTS])
+def test_integer_pattern_bf16_out_all_variants(rt, name, layout):
+    """bf16 output: interior tiles take the LDS-staged whole-row store, edge
+    tiles the direct one; both must equal RNE of the exact integer sums."""
+    m, n, k = 520, 264, 128
+    cfg = t0mi.preset(name).copy(transpose=layout)
+    a, b = int_pattern(m, k, n, layout == t0mi.NN)
+    y = run_gemm(rt, cfg, a, b, m, n, k, out_bf16=True)
+    ref = oracle.bf16_rne(oracle.gemm_bf16(a, b, "nn" if layout == t0mi.NN else "nt"))
+    assert np.array_equal(y, ref), f"{cfg.name()}: {np.count_nonzero(y != ref)} elements differ"
+
+
+@pytest.mark.parametrize("layout", [t0mi.NT, t0mi.NN])
 @pytest.mark.parametrize("sk", [2, 4, 8])
 def test_split_k_exact_and_deterministic(rt, layout, sk):
     m, n, k = 128, 256, 1024
