@@ -236,8 +236,12 @@ __global__ __launch_bounds__(512) void gemm_bf16_pingpong_kernel(GemmParams p) {
   // Every wave runs R(u) bar M(u) bar; group 1 starts one barrier later and
   // group 0 ends with one extra, so both pass 2*nk + 1 barriers.
   if (nk > 0) static_for<8>([&](auto jc) { dma(0, b_tile_of(0), jc); });
-  if (nk > 1) static_for<8>([&](auto jc) { dma(1, b_tile_of(1), jc); });
-  wait_vmcnt<0>();
+  if (nk > 1) {
+    static_for<8>([&](auto jc) { dma(1, b_tile_of(1), jc); });
+    wait_vmcnt<8>();  // tile 0 landed; tile 1 is waited for at the end of R(0)
+  } else {
+    wait_vmcnt<0>();
+  }
   bar();
   if (!g0) bar();
   int u = 0;
