@@ -13,13 +13,13 @@
 
 namespace t0mi {
 
-// The NN 256x256x64 2x4-wave configuration runs the ping-pong kernel (same
+// The 256x256x64 2x4-wave configuration runs the ping-pong kernel (same
 // results, bit for bit) whenever its K-granularity precondition holds.
 template <int BM, int BN, int BK, int WM, int WN, int S, bool NN>
 static void launch_variant(dim3 g, hipStream_t s, const GemmParams& p) {
-  if constexpr (NN && BM == 256 && BN == 256 && BK == 64 && WM == 2 && WN == 4 && S == 2) {
+  if constexpr (BM == 256 && BN == 256 && BK == 64 && WM == 2 && WN == 4 && S == 2) {
     if (pingpong_ok(p)) {
-      hipLaunchKernelGGL(gemm_bf16_pingpong_kernel<0>, g, dim3(512), 0, s, p);
+      hipLaunchKernelGGL(gemm_bf16_pingpong_kernel<NN>, g, dim3(512), 0, s, p);
       return;
     }
   }

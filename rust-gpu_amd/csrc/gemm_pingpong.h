@@ -1,10 +1,11 @@
-// gemm_pingpong.h — gfx950 bf16 GEMM, NN layout, 256x256x64 tiles, 8 waves in
+// gemm_pingpong.h — gfx950 bf16 GEMM, 256x256x64 tiles (NN and NT), 8 waves in
 // two groups that alternate between LDS reads and MFMA bursts ("ping-pong").
 //
 // Same math and the same per-accumulator MFMA order as gemm_bf16_kernel
 // <256, 256, 64, 2, 4, 2, NN> (so results are bit-identical to it); it replaces
 // that instantiation where its preconditions hold (pingpong_ok below):
-//   src/t0/gemm_gen.rs:668-1438 (generate_lds_db), NN as in BASELINE.json.
+//   src/t0/gemm_gen.rs:668-1438 (generate_lds_db): NT is the reference's
+//   layout, NN the one BASELINE.json names.
 //
 // Schedule.  Waves 0-3 (group 0) own rows 0-127 of the tile and waves 4-7
 // (group 1) rows 128-255; wave w and wave w+4 run on the same SIMD.  Every
@@ -21,16 +22,18 @@
 // 2 slots for its own half of the A tile (16 KB each; each group reads only its
 // own rows).  All global -> LDS DMA is issued inside the MFMA phases (read
 // phases are pure LDS reads):
-//   group 0, M(u): A rows 0-127 of tile u+2 and B k-rows 0-31 of tile u+2;
-//   group 1, M(u): A rows 128-255 of tile u+2 and B k-rows 32-63 of tile u+2.
+//   group 0, M(u): A rows 0-127 of tile u+2 and half of B of tile u+2;
+//   group 1, M(u): A rows 128-255 of tile u+2 and the other half
+//   (NN: B k-rows 0-31 / 32-63; NT: B rows 0-127 / 128-255).
 // The slot each DMA overwrites was last read one interval earlier, and each
 // wave waits for its DMA (vmcnt 0) at the end of its next read phase, one
 // barrier before the first wave reads it.
 //
-// Ragged edges: A is read through a buffer resource whose record count ends at
-// row M, so rows past M load as zeros; B columns past N are clamped (their
-// products land in columns that are not stored).  K (per split-K partition)
-// must be a multiple of 64 — pingpong_ok() checks it on the host.
+// Ragged edges: A (and NT's B) is read through buffer resources whose record
+// count ends at row M (N), so rows past it load as zeros; NN's B columns past N
+// are clamped (their products land in columns that are not stored).  K (per
+// split-K partition) must be a multiple of 64 — pingpong_ok() checks it on the
+// host.
 //
 // Output: full tiles with bf16 output (16-byte aligned Y) are staged through
 // LDS by store_tile_bf16_staged (each wave's 128 x 64 block, written as whole
@@ -83,7 +86,7 @@ __device__ __forceinline__ u32x4 make_rsrc(const void* base, uint32_t nbytes) {
   return r;
 }
 
-// Host-side check of the ping-pong kernel's preconditions (the NN 256x256x64
+// Host-side check of the ping-pong kernel's preconditions (the 256x256x64
 // 2x4-wave configuration is assumed by the caller).
 inline bool pingpong_ok(const GemmParams& p) {
   if (p.K == 0 || p.K % 64 != 0) return false;
@@ -92,13 +95,15 @@ inline bool pingpong_ok(const GemmParams& p) {
   return true;
 }
 
-// (A template only so that every translation unit may include the definition.)
-template <int UNUSED = 0>
+// NN: B = B[K,N] (ldb = N), LDS tile [64 k][256 n], K-contiguous operand by
+// transpose reads.  NT: B = WT[N,K] (ldb = K), LDS tile [256 n][64 k] laid out
+// and loaded like A (rows past N read zeros), fragments by ds_read_b128.
+template <bool NN>
 __global__ __launch_bounds__(512) void gemm_bf16_pingpong_kernel(GemmParams p) {
   constexpr int BK = 64, BN = 256, TN = 64;
   constexpr int FM = 4, FN = 2, KC = 8, KS = 4, NC = 32;
   constexpr int B_ELEMS = BN * BK, AH_ELEMS = 128 * BK;  // B tile, half A tile
-  constexpr int NR = FM + 2 * FN;                         // LDS reads per k-step
+  constexpr int NR = FM + (NN ? 2 * FN : FN);            // LDS reads per k-step
   __shared__ __attribute__((aligned(1024))) uint16_t smem[3 * B_ELEMS + 4 * AH_ELEMS];
 
   int tm, tn, part;
@@ -119,17 +124,22 @@ __global__ __launch_bounds__(512) void gemm_bf16_pingpong_kernel(GemmParams p) {
   // ---- DMA addressing ------------------------------------------------------
   // Wave w4 of group g fills, per tile, 1 KB blocks w4 + 4j (j = 0..3) of its
   // half of the A tile (8 rows x 64 K each) and blocks 16g + w4 + 4j of the B
-  // tile (2 k-rows x 256 columns each).  The swizzles depend on the row modulo
-  // 32 (A) and 4 (B) only, which j does not change, so one lane offset serves
-  // all four loads of a kind; j and the tile move the uniform base.
+  // tile (NN: 2 k-rows x 256 columns; NT: 8 n-rows x 64 K).  The swizzles depend
+  // on the row modulo 32 (A, NT B) or 4 (NN B) only, which j does not change, so
+  // one lane offset serves all four loads of a kind; j and the tile move the
+  // uniform base.
   uint32_t a_voff, b_voff;
   {
     const int row = w4 * 8 + (lane >> 3), pc = lane & 7;
     a_voff = (uint32_t)(row * (int)p.lda + ((pc ^ swz<KC>(row)) * 8)) * 2u;
-    const int brow = 2 * (16 * g + w4) + (lane >> 5), bpc = lane & 31;
-    int gn = n0 + ((bpc ^ swz_nn<NC>(brow)) * 8);
-    gn = gn < (int)p.N ? gn : (int)p.N - 8;
-    b_voff = (uint32_t)(brow * (int)p.ldb + gn) * 2u;
+    if constexpr (NN) {
+      const int brow = 2 * (16 * g + w4) + (lane >> 5), bpc = lane & 31;
+      int gn = n0 + ((bpc ^ swz_nn<NC>(brow)) * 8);
+      gn = gn < (int)p.N ? gn : (int)p.N - 8;
+      b_voff = (uint32_t)(brow * (int)p.ldb + gn) * 2u;
+    } else {
+      b_voff = (uint32_t)(row * (int)p.ldb + ((pc ^ swz<KC>(row)) * 8)) * 2u;
+    }
   }
   // A through four buffer resources, one per 32-row block j of this group's
   // half, fixed for the whole K loop: base = row block start, record count =
@@ -138,37 +148,51 @@ __global__ __launch_bounds__(512) void gemm_bf16_pingpong_kernel(GemmParams p) {
   // rows stay in range and rows past M out of range whether or not the range
   // check counts that operand (k0 + 64 <= K <= lda).
   const uint64_t a_row_bytes = (uint64_t)p.lda * 2u;
+  const uint64_t b_row_bytes = (uint64_t)p.ldb * 2u;
+  // Row block [r0, r0 + 32) of a row-major [rows][ld] operand; the base is not
+  // dereferenced when the record count is 0.
+  auto block_rsrc = [](const uint16_t* base, int rows, int r0, uint64_t row_bytes) {
+    const int left_rows = rows - r0;
+    const uint64_t left = left_rows <= 0 ? 0u : (uint64_t)left_rows * row_bytes;
+    return make_rsrc((const char*)base + (uint64_t)r0 * row_bytes, left > 0x7fffffffu ? 0x7fffffffu : (uint32_t)left);
+  };
   u32x4 a_rs[4];
 #pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    const int rows = (int)p.M - (m0 + g * 128 + j * 32);
-    const uint64_t left = rows <= 0 ? 0u : (uint64_t)rows * a_row_bytes;
-    // The base is not dereferenced when the record count is 0.
-    a_rs[j] = make_rsrc((const char*)p.a + (uint64_t)(m0 + g * 128 + j * 32) * a_row_bytes,
-                        left > 0x7fffffffu ? 0x7fffffffu : (uint32_t)left);
+  for (int j = 0; j < 4; ++j) a_rs[j] = block_rsrc(p.a, (int)p.M, m0 + g * 128 + j * 32, a_row_bytes);
+  // NT: B rows (n) the same way, so rows past N read zeros.
+  u32x4 b_rs[NN ? 1 : 4];
+  if constexpr (!NN) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) b_rs[j] = block_rsrc(p.b, (int)p.N, n0 + g * 128 + j * 32, b_row_bytes);
   }
-  const uint64_t b_row_bytes = (uint64_t)p.ldb * 2u;
   const uint32_t b_lds0 = smem_base + (16 * g + w4) * 1024;
   const uint32_t a_lds0 = a_slot0 + w4 * 1024;
-  // DMA j of tile t: j < 4 from A row block j, else B k-rows 8(j-4) .. +1 of the
-  // wave's B block (the tile's base address is formed once per phase).
+  // DMA j of tile t: j < 4 from A row block j; else NN: B k-rows 8(j-4) .. +1
+  // of the wave's B block (the tile's base address is formed once per phase),
+  // NT: B row block j-4.
   auto dma = [&](int t, const char* b_tile, auto jc) {
     constexpr int j = decltype(jc)::value;
     if constexpr (j < 4) {
       lds_dma16_rsrc(a_rs[j], a_voff, (uint32_t)(kbeg + t * BK) * 2u,
                      a_lds0 + (uint32_t)((t & 1) * AH_ELEMS * 2) + 4 * j * 1024);
-    } else {
+    } else if constexpr (NN) {
       lds_dma16_sv(b_tile + (uint64_t)(j - 4) * 8u * b_row_bytes, b_voff,
                    b_lds0 + (uint32_t)((t % 3) * B_ELEMS * 2) + 4 * (j - 4) * 1024);
+    } else {
+      lds_dma16_rsrc(b_rs[j - 4], b_voff, (uint32_t)(kbeg + t * BK) * 2u,
+                     b_lds0 + (uint32_t)((t % 3) * B_ELEMS * 2) + 4 * (j - 4) * 1024);
     }
   };
-  auto b_tile_of = [&](int t) { return (const char*)p.b + (uint64_t)(kbeg + t * BK) * b_row_bytes; };
+  auto b_tile_of = [&](int t) { return NN ? (const char*)p.b + (uint64_t)(kbeg + t * BK) * b_row_bytes : nullptr; };
 
   // ---- LDS -> fragments (same addressing as gemm_bf16_kernel, NN) -----------
   const int lrow = lane & 31, lhalf = lane >> 5;
-  int a_off[KS];
+  int a_off[KS], b_off[NN ? 1 : KS];
 #pragma unroll
-  for (int ks = 0; ks < KS; ++ks) a_off[ks] = lrow * BK + (((ks * 2 + lhalf) ^ swz<KC>(lrow)) * 8);
+  for (int ks = 0; ks < KS; ++ks) {
+    a_off[ks] = lrow * BK + (((ks * 2 + lhalf) ^ swz<KC>(lrow)) * 8);
+    if constexpr (!NN) b_off[ks] = (wn * TN + lrow) * BK + (((ks * 2 + lhalf) ^ swz<KC>(lrow)) * 8);
+  }
   const int tg = lane >> 4, ti = lane & 15;
   const int nn_krow0 = 8 * (tg >> 1) + (ti >> 2);
   const int nn_col0 = wn * TN + 16 * (tg & 1) + 4 * (ti & 3);
@@ -181,6 +205,8 @@ __global__ __launch_bounds__(512) void gemm_bf16_pingpong_kernel(GemmParams p) {
     constexpr int ks = i / NR, r = i % NR;
     if constexpr (r < FM) {
       xa[ks][r] = *(const bf16x8*)(As + a_off[ks] + r * 32 * BK);
+    } else if constexpr (!NN) {
+      xb[ks][r - FM] = *(const bf16x8*)(Bs + b_off[ks] + (r - FM) * 32 * BK);
     } else {
       constexpr int fn = (r - FM) / 2, h = (r - FM) % 2;
       const int col = nn_col0 + fn * 32;

@@ -1,6 +1,6 @@
-"""GPU parity tests of the ping-pong schedule of the NN 256x256x64 2x4-wave GEMM
-configuration (csrc/gemm_pingpong.h), which replaces the generic kernel for
-that configuration when K (per split-K partition) is a multiple of 64.
+"""GPU parity tests of the ping-pong schedule of the 256x256x64 2x4-wave GEMM
+configuration (csrc/gemm_pingpong.h), NN and NT, which replaces the generic
+kernel for that configuration when K (per split-K partition) is a multiple of 64.
 
 Bars:
   - bit-identical to the generic kernel of the same configuration: the generic
@@ -39,9 +39,9 @@ def rand_bf16(shape, seed):
     return oracle.bf16_trunc(g.standard_normal(shape).astype(np.float32))
 
 
-def run(rt, a, b, m, n, k, out_bf16, split_k=1, epilogue=None, bias=None):
+def run(rt, a, b, m, n, k, out_bf16, split_k=1, epilogue=None, bias=None, layout=t0mi.NN):
     cfg = t0mi.preset("gfx950_256x256_k64_w2x4").copy(
-        transpose=t0mi.NN, split_k=split_k, out_dtype=t0mi.OUT_BF16 if out_bf16 else t0mi.OUT_F32)
+        transpose=layout, split_k=split_k, out_dtype=t0mi.OUT_BF16 if out_bf16 else t0mi.OUT_F32)
     if epilogue is not None:
         cfg = cfg.copy(epilogue=epilogue)
     da, pa = to_dev(a)
@@ -55,13 +55,25 @@ def run(rt, a, b, m, n, k, out_bf16, split_k=1, epilogue=None, bias=None):
     return from_dev(dy, np.uint16 if out_bf16 else np.float32, (m, n))
 
 
-def run_generic(rt, a, b, m, n, k, out_bf16, **kw):
+def run_generic(rt, a, b, m, n, k, out_bf16, layout=t0mi.NN, **kw):
     """Same problem through the generic kernel: K + 8 with zero padding."""
     ap = np.zeros((m, k + 8), np.uint16)
     ap[:, :k] = a
-    bp = np.zeros((k + 8, n), np.uint16)
-    bp[:k] = b
-    return run(rt, ap, bp, m, n, k + 8, out_bf16, **kw)
+    if layout == t0mi.NN:
+        bp = np.zeros((k + 8, n), np.uint16)
+        bp[:k] = b
+    else:
+        bp = np.zeros((n, k + 8), np.uint16)
+        bp[:, :k] = b
+    return run(rt, ap, bp, m, n, k + 8, out_bf16, layout=layout, **kw)
+
+
+def rand_b(layout, n, k, seed):
+    return rand_bf16((k, n) if layout == t0mi.NN else (n, k), seed)
+
+
+def lname(layout):
+    return "nn" if layout == t0mi.NN else "nt"
 
 
 def bf16_to_f32(u16):
@@ -72,7 +84,7 @@ CASES = [
     # (m, n, k, out_bf16, split_k)
     (512, 512, 256, True, 1),     # full tiles, staged store
     (300, 512, 192, True, 1),     # ragged M: tile row 1 has 44 rows, its group 1 has none
-    (512, 392, 128, True, 1),     # ragged N: clamped B columns
+    (512, 392, 128, True, 1),     # ragged N: clamped B columns (NN), zero rows (NT)
     (260, 264, 64, False, 1),     # one K tile, both ragged, f32 out
     (256, 256, 8192, True, 1),    # long K
     (256, 512, 1024, False, 4),   # split-K f32 planes (256 per partition)
@@ -80,18 +92,19 @@ CASES = [
 ]
 
 
+@pytest.mark.parametrize("layout", [t0mi.NN, t0mi.NT])
 @pytest.mark.parametrize("m,n,k,out_bf16,sk", CASES)
-def test_bit_identical_to_generic_kernel(rt, m, n, k, out_bf16, sk):
+def test_bit_identical_to_generic_kernel(rt, m, n, k, out_bf16, sk, layout):
     a = rand_bf16((m, k), 11 + m)
-    b = rand_bf16((k, n), 23 + n)
-    y = run(rt, a, b, m, n, k, out_bf16, split_k=sk)
+    b = rand_b(layout, n, k, 23 + n)
+    y = run(rt, a, b, m, n, k, out_bf16, split_k=sk, layout=layout)
     if sk == 1:
-        y_gen = run_generic(rt, a, b, m, n, k, out_bf16)
+        y_gen = run_generic(rt, a, b, m, n, k, out_bf16, layout=layout)
         assert np.array_equal(y, y_gen), f"{(m, n, k)}: {np.count_nonzero(y != y_gen)} elements differ"
     else:
-        assert np.array_equal(y, run(rt, a, b, m, n, k, out_bf16, split_k=sk)), "split-K is deterministic"
+        assert np.array_equal(y, run(rt, a, b, m, n, k, out_bf16, split_k=sk, layout=layout)), "deterministic"
     # And against the oracle, within the GEMM tolerance.
-    ref = oracle.gemm_bf16(a, b, "nn")
+    ref = oracle.gemm_bf16(a, b, lname(layout))
     got = bf16_to_f32(y) if out_bf16 else y
     amax = np.abs(bf16_to_f32(a)).max()
     bmax = np.abs(bf16_to_f32(b)).max()
@@ -99,28 +112,31 @@ def test_bit_identical_to_generic_kernel(rt, m, n, k, out_bf16, sk):
     assert np.abs(got - ref).max() <= tol
 
 
+@pytest.mark.parametrize("layout", [t0mi.NN, t0mi.NT])
 @pytest.mark.parametrize("m,n,k", [(512, 512, 128), (300, 392, 192)])
-def test_integer_pattern_exact(rt, m, n, k):
+def test_integer_pattern_exact(rt, m, n, k, layout):
     a = oracle.bf16_trunc(((np.arange(m * k) % 7) - 3).astype(np.float32).reshape(m, k))
-    b = oracle.bf16_trunc(((np.arange(k * n) % 5) - 2).astype(np.float32).reshape(k, n))
-    y = run(rt, a, b, m, n, k, False)
-    assert np.array_equal(y, oracle.gemm_bf16(a, b, "nn"))
-    yb = run(rt, a, b, m, n, k, True)
-    assert np.array_equal(yb, oracle.bf16_rne(oracle.gemm_bf16(a, b, "nn")))
+    b = oracle.bf16_trunc(((np.arange(k * n) % 5) - 2).astype(np.float32))
+    b = b.reshape((k, n) if layout == t0mi.NN else (n, k))
+    y = run(rt, a, b, m, n, k, False, layout=layout)
+    assert np.array_equal(y, oracle.gemm_bf16(a, b, lname(layout)))
+    yb = run(rt, a, b, m, n, k, True, layout=layout)
+    assert np.array_equal(yb, oracle.bf16_rne(oracle.gemm_bf16(a, b, lname(layout))))
 
 
+@pytest.mark.parametrize("layout", [t0mi.NN, t0mi.NT])
 @pytest.mark.parametrize("epi", [t0mi.EPI_BIAS_ADD, t0mi.EPI_BIAS_ADD_RELU])
 @pytest.mark.parametrize("m,n,out_bf16", [(512, 512, True), (264, 392, True), (512, 256, False)])
-def test_bias_epilogue(rt, m, n, out_bf16, epi):
+def test_bias_epilogue(rt, m, n, out_bf16, epi, layout):
     """GemmConfig epilogues (src/t0/gemm_gen.rs:41-49), applied before the staged store."""
     k = 256
     a = rand_bf16((m, k), 5)
-    b = rand_bf16((k, n), 6)
+    b = rand_b(layout, n, k, 6)
     bias = np.linspace(-1.0, 1.0, n).astype(np.float32)
-    y = run(rt, a, b, m, n, k, out_bf16, epilogue=epi, bias=bias)
-    y_gen = run_generic(rt, a, b, m, n, k, out_bf16, epilogue=epi, bias=bias)
+    y = run(rt, a, b, m, n, k, out_bf16, epilogue=epi, bias=bias, layout=layout)
+    y_gen = run_generic(rt, a, b, m, n, k, out_bf16, epilogue=epi, bias=bias, layout=layout)
     assert np.array_equal(y, y_gen)
-    ref = oracle.gemm_bf16(a, b, "nn") + bias
+    ref = oracle.gemm_bf16(a, b, lname(layout)) + bias
     if epi == t0mi.EPI_BIAS_ADD_RELU:
         ref = np.maximum(ref, 0.0)
     got = bf16_to_f32(y) if out_bf16 else y
