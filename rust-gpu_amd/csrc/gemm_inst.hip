@@ -1,5 +1,5 @@
 // gemm_inst.hip — instantiates one block of gemm_variants.def for one B layout.
-// Compiled six times by the build (T0MI_PART = 0/1/2, T0MI_INST_NN = 0/1, with
+// Compiled eight times by the build (T0MI_PART = 0..3, T0MI_INST_NN = 0/1, with
 // T0MI_TABLE_FN naming the table accessor) so the variants build in parallel.
 #include "gemm_pingpong.h"
 #include "t0mi_ctx.h"

@@ -26,6 +26,8 @@ const GemmLaunchEntry* gemm_table_p0_nn(size_t* n);
 const GemmLaunchEntry* gemm_table_p1_nn(size_t* n);
 const GemmLaunchEntry* gemm_table_p2_nt(size_t* n);
 const GemmLaunchEntry* gemm_table_p2_nn(size_t* n);
+const GemmLaunchEntry* gemm_table_p3_nt(size_t* n);
+const GemmLaunchEntry* gemm_table_p3_nn(size_t* n);
 const GemmLaunchEntry* find_gemm_launch(const t0mi_gemm_config& c);
 
 enum KernelKind : int { KK_GEMM_GEN = 1, KK_TILE = 2 };

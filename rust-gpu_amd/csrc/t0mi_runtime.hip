@@ -27,7 +27,8 @@ const GemmLaunchEntry* find_gemm_launch(const t0mi_gemm_config& c) {
   const bool nn = c.transpose == T0MI_NN;
   const GemmLaunchEntry* (*tables[])(size_t*) = {nn ? gemm_table_p0_nn : gemm_table_p0_nt,
                                                 nn ? gemm_table_p1_nn : gemm_table_p1_nt,
-                                                nn ? gemm_table_p2_nn : gemm_table_p2_nt};
+                                                nn ? gemm_table_p2_nn : gemm_table_p2_nt,
+                                                nn ? gemm_table_p3_nn : gemm_table_p3_nt};
   for (auto tf : tables) {
     size_t n = 0;
     const GemmLaunchEntry* t = tf(&n);
