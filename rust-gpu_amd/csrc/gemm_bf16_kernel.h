@@ -9,10 +9,11 @@
 //     each wave instruction fills one contiguous 1 KB LDS block, so the LDS
 //     swizzle is applied on the global side (each lane fetches the chunk that
 //     belongs at its LDS slot);
-//   * a ring of S = 2..5 LDS stages, one barrier per K tile: tile it+S-1 is
-//     requested before tile it's MFMAs, and waits count outstanding DMA
-//     instructions (vmcnt) so up to S-1 tiles are in flight; with S >= 3 the
-//     first fragments of tile it+1 are read during tile it's last k-step;
+//   * a ring of S = 2..5 LDS stages, one barrier per K tile; waits count
+//     outstanding DMA instructions (vmcnt) so up to S-1 tiles are in flight,
+//     and with S >= 3 each tile's loads are spread over the previous tile's
+//     k-steps; the first fragments of tile it+1 are read during tile it's last
+//     k-step;
 //   * v_mfma_f32_32x32x16_bf16 with the A and B fragments of the next k-step
 //     read from LDS while the current k-step's MFMAs run.
 //
@@ -513,27 +514,39 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_bf16_kernel(GemmParams p) {
     if (NREAD > NMFMA) __builtin_amdgcn_sched_group_barrier(0x100, NREAD - NMFMA, 0);
   };
 
-  // Ring of S stages; tile t lives in stage t % S.  The prologue requests
-  // tiles 0 .. S-1.  In iteration `it` the wave runs k-steps 0 .. KS-2 of tile
-  // `it`, then waits for its own DMA of tile it+1 and meets the other waves at
-  // the barrier, which (a) publishes tile it+1 and (b) proves every wave has
-  // read all of stage it % S (the fragments of the last k-step are already in
-  // registers).  Stage it % S then receives tile it+S, and the first
-  // fragments of tile it+1 are read while the last k-step's MFMAs run, so the
-  // MFMA stream does not drain at tile boundaries.  Tiles it+1 .. it+S are in
-  // flight while tile `it` is computed.
+  // Ring of S stages; tile t lives in stage t % S.  In iteration `it` the wave
+  // runs k-steps 0 .. KS-2 of tile `it`, then waits for its own DMA of tile
+  // it+1 and meets the other waves at the barrier, which (a) publishes tile
+  // it+1 and (b) proves every wave has read all of stage it % S (the fragments
+  // of the last k-step are already in registers).  The first fragments of tile
+  // it+1 are read while the last k-step's MFMAs run, so the MFMA stream does not
+  // drain at tile boundaries.  Where the DMA goes:
+  //   S = 2 (or an uneven DMA split): the prologue requests tiles 0 .. S-1 and
+  //   stage it % S receives tile it+S after the barrier, during the last
+  //   k-step;
+  //   S >= 3 with an even split ("spread"): the prologue requests tiles
+  //   0 .. S-2 and iteration `it` loads tile it+S-1 into stage (it-1) % S,
+  //   free since the previous barrier, with the loads spread one per MFMA
+  //   slot over all KS k-steps (load j in k-step j*KS/LPT).  A CU accepts a
+  //   1 KB load only every ~22 cycles, so a whole tile's DMA squeezed into one
+  //   k-step stalls the issuing wave; spread, the same loads cost 1.5-3.5 %
+  //   less time (bit-identical results).
   // vmcnt arithmetic: with an even DMA split every wave issues LPT loads per
-  // tile, so "tile it+1 landed" is vmcnt <= LPT * (number of younger tiles in
-  // flight); otherwise, and near the end of K, the wave waits for all loads.
+  // tile, so "tile it+1 landed" is vmcnt <= the number of loads issued after
+  // it (S = 2: LPT * (S-2); spread: LPT * (S-3) + the loads of tile it+S-1
+  // issued before the barrier); otherwise, and near the end of K, the wave
+  // waits for all loads.
   constexpr int LPT = T::LPT;
   constexpr bool EVEN = T::EVEN;
   bf16x8 xa[2][FM], xb[2][FN];
+  constexpr bool SPREAD = EVEN && S >= 3;
+  constexpr int PRO = SPREAD ? S - 1 : S;  // tiles loaded by the prologue
   if (nk > 0) {
 #pragma unroll
-    for (int t = 0; t < S; ++t)
+    for (int t = 0; t < PRO; ++t)
       if (t < nk) load_tile(t, t);
-    if (EVEN && nk >= S)
-      wait_vmcnt<EVEN ? LPT * (S - 1) : 0>();
+    if (EVEN && nk >= PRO)
+      wait_vmcnt<EVEN ? LPT * (PRO - 1) : 0>();
     else
       wait_vmcnt<0>();
     __syncthreads();
@@ -543,28 +556,52 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_bf16_kernel(GemmParams p) {
   // One iteration; BARRIER: not the last tile; LOAD: tile it+S exists.  The
   // three loop copies below keep each body free of branches, so the compiler's
   // LDS wait counts never merge the next tile's reads into the current ones.
+  // Spread DMA: tile it+S-1 goes into stage (it-1) % S (free since the previous
+  // barrier); load j is issued in k-step j*KS/LPT, one per MFMA slot.
+  constexpr int PRE = SPREAD ? (LPT * (KS - 1) + KS - 1) / KS : 0;  // loads j with j*KS/LPT < KS-1
   auto iteration = [&](int it, auto barrier_c, auto load_c, auto check_c) {
     constexpr bool BARRIER = decltype(barrier_c)::value, LOAD = decltype(load_c)::value;
     const uint16_t* cur = smem + (it % S) * BUF;
-#pragma unroll
-    for (int ks = 0; ks + 1 < KS; ++ks) {
-      const int c = ks & 1;
-      read_frags(cur, ks + 1, xa[c ^ 1], xb[c ^ 1]);
-      mfma_step(xa[c], xb[c]);
-      interleave_hint();
-    }
+    const int lt = SPREAD ? it + S - 1 : it + S;          // tile loaded by this iteration
+    const int ls = SPREAD ? (it + S - 1) % S : it % S;    // its stage
+    static_for<KS - 1>([&](auto ksc) {
+      constexpr int ks = decltype(ksc)::value;
+      constexpr int c = ks & 1;
+      if constexpr (SPREAD && LOAD) {
+        // reads of k-step ks+1, this k-step's MFMAs, and its DMA loads, one per slot
+        constexpr int J0 = (ks * LPT + KS - 1) / KS, J1 = ((ks + 1) * LPT + KS - 1) / KS;  // j in [J0, J1)
+        constexpr int NJ = J1 - J0;
+        constexpr int NMEM2 = NJ > NREAD ? NJ : NREAD;
+        constexpr int NSL = NMFMA > NMEM2 ? NMFMA : NMEM2;
+        static_for<NSL>([&](auto ic) {
+          constexpr int i = decltype(ic)::value;
+          if constexpr (i < NMFMA) {
+            constexpr int fn = i / FM, fm = i % FM;
+            acc[fn][fm] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(xb[c][fn], xa[c][fm], acc[fn][fm], 0, 0, 0);
+          }
+          if constexpr (i < NJ) dma_one(lt, ls, std::integral_constant<int, J0 + i>{}, check_c);
+          if constexpr (i < NREAD) read_one(cur, ks + 1, std::integral_constant<int, i>{}, xa[c ^ 1], xb[c ^ 1]);
+          __builtin_amdgcn_sched_barrier(0);
+        });
+      } else {
+        read_frags(cur, ks + 1, xa[c ^ 1], xb[c ^ 1]);
+        mfma_step(xa[c], xb[c]);
+        interleave_hint();
+      }
+    });
     if constexpr (BARRIER) {
-      if constexpr (LOAD && EVEN)
+      if constexpr (SPREAD && LOAD)
+        wait_vmcnt<SPREAD ? LPT * (S - 3) + PRE : 0>();  // tile it+1 landed
+      else if constexpr (!SPREAD && LOAD && EVEN)
         wait_vmcnt<EVEN ? LPT * (S - 2) : 0>();  // tile it+1 landed, it+2 .. it+S-1 may fly
       else
         wait_vmcnt<0>();
-      wait_lgkmcnt0();  // this wave's reads of stage it % S are complete
+      wait_lgkmcnt0();
       __syncthreads();
-      // The last k-step's MFMAs with the DMA loads of tile it+S and the reads
-      // of tile it+1's first k-step placed one per MFMA, in this order (the
-      // scheduler may not move anything across the sched_barriers).
       const uint16_t* nxt = smem + ((it + 1) % S) * BUF;
-      constexpr int NMEM = NDMA > NREAD ? NDMA : NREAD;
+      constexpr int JL = SPREAD ? PRE : 0;
+      constexpr int NDL = NDMA - JL;  // loads left for the last k-step
+      constexpr int NMEM = NDL > NREAD ? NDL : NREAD;
       constexpr int NSLOT = NMFMA > NMEM ? NMFMA : NMEM;
       static_for<NSLOT>([&](auto ic) {
         constexpr int i = decltype(ic)::value;
@@ -573,7 +610,7 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_bf16_kernel(GemmParams p) {
           acc[fn][fm] =
               __builtin_amdgcn_mfma_f32_32x32x16_bf16(xb[CL][fn], xa[CL][fm], acc[fn][fm], 0, 0, 0);
         }
-        if constexpr (LOAD && i < NDMA) dma_one(it + S, it % S, std::integral_constant<int, i>{}, check_c);
+        if constexpr (LOAD && i < NDL) dma_one(lt, ls, std::integral_constant<int, JL + i>{}, check_c);
         if constexpr (i < NREAD) read_one(nxt, 0, std::integral_constant<int, i>{}, xa[CL ^ 1], xb[CL ^ 1]);
         __builtin_amdgcn_sched_barrier(0);
       });
@@ -581,7 +618,6 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_bf16_kernel(GemmParams p) {
       mfma_step(xa[CL], xb[CL]);
     }
     if constexpr (CL == 0) {
-      // Odd KS: tile it+1 starts in buffer 0.
 #pragma unroll
       for (int f = 0; f < FM; ++f) xa[0][f] = xa[1][f];
 #pragma unroll
@@ -592,8 +628,9 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_bf16_kernel(GemmParams p) {
   using False = std::integral_constant<bool, false>;
   const int nfull = kspan / BK;  // tiles that end inside the K range
   int it = 0;
-  for (; it + S < nfull; ++it) iteration(it, True{}, True{}, False{});  // steady state
-  for (; it + S < nk; ++it) iteration(it, True{}, True{}, True{});      // loads the partial last tile
+  constexpr int AHEAD = SPREAD ? S - 1 : S;  // iteration it loads tile it + AHEAD
+  for (; it + AHEAD < nfull; ++it) iteration(it, True{}, True{}, False{});  // steady state
+  for (; it + AHEAD < nk; ++it) iteration(it, True{}, True{}, True{});      // loads the partial last tile
   for (; it + 1 < nk; ++it) iteration(it, True{}, False{}, False{});
   if (it < nk) iteration(it, False{}, False{}, False{});
 
