@@ -142,3 +142,33 @@ def test_bias_epilogue(rt, m, n, out_bf16, epi, layout):
     got = bf16_to_f32(y) if out_bf16 else y
     tol = 1e-2 * np.sqrt(k) * np.abs(bf16_to_f32(a)).max() * np.abs(bf16_to_f32(b)).max()
     assert np.abs(got - ref).max() <= tol
+
+
+@pytest.mark.parametrize("preset", ["gfx950_256x256_k64_w2x4", "gfx950_128x128_k64_w2x2"])
+def test_bf16_out_to_8_byte_aligned_y(rt, preset):
+    """t0mi_gemm refuses a Y that is not 16-byte aligned; the reference's raw
+    dispatch path (gemm_gen kernargs, gpu_context.rs:305-357) checks no
+    alignment, so there full tiles with an 8-byte aligned bf16 Y take the
+    direct store instead of the staged one (16 bytes per lane), with the same
+    results as an aligned Y."""
+    m, n, k = 512, 512, 128
+    a = rand_bf16((m, k), 31)
+    b = rand_bf16((k, n), 32)
+    cfg = t0mi.preset(preset).copy(transpose=t0mi.NN, out_dtype=t0mi.OUT_BF16)
+    da, pa = to_dev(a)
+    db, pb = to_dev(b)
+    dy, py = empty_dev(m * n * 2 + 16, fill=0xAB)
+    with pytest.raises(t0mi.T0miError) as e:
+        rt.gemm(cfg, pa, pb, py + 8, m, n, k)
+    assert e.value.code == t0mi.ERR_INVALID
+    kern = rt.kernel(cfg)
+    grid = t0mi.compute_grid_auto(cfg, m, n)
+    assert rt.dispatch(kern, grid, t0mi.build_kernargs(pa, pb, py, k, n, m, cfg)) == t0mi.OK
+    aligned = from_dev(dy, np.uint16, (m, n))
+    tol = 1e-2 * np.sqrt(k) * np.abs(bf16_to_f32(a)).max() * np.abs(bf16_to_f32(b)).max()
+    assert np.abs(bf16_to_f32(aligned) - oracle.gemm_bf16(a, b, "nn")).max() <= tol
+    dy2, py2 = empty_dev(m * n * 2 + 16, fill=0xAB)
+    assert rt.dispatch(kern, grid, t0mi.build_kernargs(pa, pb, py2 + 8, k, n, m, cfg)) == t0mi.OK
+    raw = from_dev(dy2, np.uint8, (m * n * 2 + 16,))
+    assert np.all(raw[:8] == 0xAB) and np.all(raw[8 + m * n * 2:] == 0xAB)
+    assert np.array_equal(raw[8:8 + m * n * 2].view(np.uint16).reshape(m, n), aligned)
