@@ -149,8 +149,9 @@ __global__ __launch_bounds__(512) void gemm_bf16_pingpong_kernel(GemmParams p) {
   // check counts that operand (k0 + 64 <= K <= lda).
   const uint64_t a_row_bytes = (uint64_t)p.lda * 2u;
   const uint64_t b_row_bytes = (uint64_t)p.ldb * 2u;
-  // Row block [r0, r0 + 32) of a row-major [rows][ld] operand; the base is not
-  // dereferenced when the record count is 0.
+  // Resource based at row r0 of a row-major [rows][ld] operand whose record
+  // count ends with row rows-1 (0 when r0 >= rows; the base is then never
+  // dereferenced).
   auto block_rsrc = [](const uint16_t* base, int rows, int r0, uint64_t row_bytes) {
     const int left_rows = rows - r0;
     const uint64_t left = left_rows <= 0 ? 0u : (uint64_t)left_rows * row_bytes;
@@ -167,9 +168,9 @@ __global__ __launch_bounds__(512) void gemm_bf16_pingpong_kernel(GemmParams p) {
   }
   const uint32_t b_lds0 = smem_base + (16 * g + w4) * 1024;
   const uint32_t a_lds0 = a_slot0 + w4 * 1024;
-  // DMA j of tile t: j < 4 from A row block j; else NN: B k-rows 8(j-4) .. +1
-  // of the wave's B block (the tile's base address is formed once per phase),
-  // NT: B row block j-4.
+  // DMA j of tile t: j < 4 from A row block j; else NN: the wave's B block
+  // 16g + w4 + 4(j-4), i.e. k-rows 2(16g + w4) + 8(j-4) and the next (the
+  // tile's base address is formed once per phase); NT: B row block j-4.
   auto dma = [&](int t, const char* b_tile, auto jc) {
     constexpr int j = decltype(jc)::value;
     if constexpr (j < 4) {
