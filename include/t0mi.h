@@ -383,12 +383,15 @@ int t0mi_auto_gemm(t0mi_ctx* ctx, uint64_t a, uint64_t b, uint64_t c, uint32_t m
  * Requires k % group == 0, group % 32 == 0, n % 8 == 0; A and qweight 16-byte
  * aligned, scales and Y 8-byte aligned.  Asynchronous.
  * Routes by row count: up to 80 rows the decode kernel per 16-row slab (exact
- * dequant inside the MFMA); 81..767 rows the fused tile kernel (the weight is
- * rounded once to bf16 before the MFMA), K split through the library
- * workspace when tiles are fewer than CUs; from 768 rows, and from 81 rows for
- * a group that is not a power of two, the weight is dequantized once to bf16
- * into the library's conversion buffer (k * n * 2 bytes, kept by the runtime)
- * and the dense NN GEMM runs. */
+ * dequant inside the MFMA); then kernels that dequantize inside the MFMA K
+ * loop, rounding the weight once to bf16: 81..191 rows the 128x128 fused tile
+ * kernel, 192..1535 rows (K and group multiples of 64) the 256x256 ping-pong
+ * kernel, K split through the library workspace when tiles are fewer than
+ * CUs; from 1536 rows (768 when K or the group is not a multiple of 64, and
+ * from 81 rows for a group that is not a power of two) the weight is
+ * dequantized once to bf16 into the library's conversion buffer (k * n * 2
+ * bytes, kept by the runtime) and the dense NN GEMM runs.  The ping-pong and
+ * the dequant-once routes give bit-identical results on the same problem. */
 int t0mi_w4a16_gemm(t0mi_ctx* ctx, uint64_t a, uint64_t qweight, uint64_t scales, uint64_t qzeros,
                     uint32_t zp_const, uint64_t y, uint32_t m, uint32_t k, uint32_t n, uint32_t group,
                     uint32_t out_dtype);

@@ -22,6 +22,7 @@
 
 #include "t0mi_ctx.h"
 #include "w4a16_decode.h"
+#include "w4a16_pingpong.h"
 #include "w4a16_prefill.h"
 
 using namespace t0mi;
@@ -329,15 +330,24 @@ static int hip_fail(hipError_t e, const char* what) {
   return set_error(T0MI_ERR_HIP, "%s: %s", what, hipGetErrorString(e));
 }
 
-// Up to this many rows the decode kernel runs once per 16-row slab (measured
-// at K = 4096, N = 11008 and 14336: 5 slabs cost about one launch of the
-// fused kernel, whose dequant work per workgroup does not shrink with M); above it the MFMA
-// prefill kernel, and from kTwoPassRows rows on the weights are dequantized
-// once to bf16 and the dense NN GEMM runs: the dequant pass (0.5 B read + 2 B
-// written per weight, at HBM speed) then costs less than dequantizing inside
-// every M tile's K-loop.
+// Routes by row count (measured at K = 4096, N = 11008 and 14336):
+//  - up to kDecodeMaxRows the decode kernel runs once per 16-row slab (5 slabs
+//    cost about one launch of a fused kernel, whose dequant work per workgroup
+//    does not shrink with M);
+//  - then the 128x128 fused prefill kernel (w4a16_prefill.h) up to
+//    kPingPongRows - 1 (128 rows: 40 us against 42 us for the ping-pong kernel);
+//  - then, when K and the group are multiples of 64, the fused ping-pong kernel
+//    (w4a16_pingpong.h) below kTwoPassRows (512 rows: 81 us; the other routes
+//    98-101 us);
+//  - from kTwoPassRows rows on (and for groups the fused kernels do not take)
+//    the weights are dequantized once to bf16 and the dense NN GEMM runs: the
+//    dequant pass (0.5 B read + 2 B written per weight, at HBM speed) then costs
+//    less than dequantizing inside every M tile's K-loop, which is VALU work
+//    (2048 rows: 224 us two-pass against 232 us fused; 4096 rows: 414 vs 457).
 static constexpr uint32_t kDecodeMaxRows = 80;
-static constexpr uint32_t kTwoPassRows = 768;
+static constexpr uint32_t kPingPongRows = 192;
+static constexpr uint32_t kTwoPassRows = 1536;
+static constexpr uint32_t kPrefillTwoPassRows = 768;  // groups or K the ping-pong kernel does not take
 
 static int launch_dequant(t0mi_ctx* ctx, uint64_t qweight, uint64_t scales, uint64_t qzeros, uint32_t zp_const,
                           uint64_t out, uint32_t k, uint32_t n, uint32_t group, uint32_t round_mode) {
@@ -346,6 +356,57 @@ static int launch_dequant(t0mi_ctx* ctx, uint64_t qweight, uint64_t scales, uint
                      (const uint16_t*)scales, (const uint32_t*)qzeros, zp_const, (void*)out, k, n, group, round_mode);
   hipError_t e = hipGetLastError();
   return e == hipSuccess ? T0MI_OK : hip_fail(e, "dequant launch");
+}
+
+// The fused ping-pong kernel (w4a16_pingpong.h): 256x256 tiles, K split so
+// that the workgroups cover the CUs when the tiles do not; partial planes are
+// summed in partition order by the split-K reduce.  Callers check
+// w4_pingpong_ok(k, group, ...) for whole 64-K tiles and groups.
+static int launch_w4_pingpong(t0mi_ctx* ctx, uint64_t a, uint64_t qweight, uint64_t scales, uint64_t qzeros,
+                              uint32_t zp_const, uint64_t y, uint32_t m, uint32_t k, uint32_t n, uint32_t group,
+                              bool out_bf16) {
+  W4PPParams q;
+  memset(&q, 0, sizeof q);
+  GemmParams& g = q.g;
+  g.a = (const uint16_t*)a;
+  g.y = (void*)y;
+  g.M = m;
+  g.N = n;
+  g.K = k;
+  g.lda = k;
+  g.ldy = n;
+  g.tiles_m = (m + 255) / 256;
+  g.tiles_n = (n + 255) / 256;
+  g.xcd_remap = 1;
+  g.out_bf16 = out_bf16;
+  const uint32_t tiles = g.tiles_m * g.tiles_n, nk_all = k / 64;
+  uint32_t sk = std::max(1u, std::min(8u, (uint32_t)ctx->cu_count / std::max(1u, tiles)));
+  sk = std::min(sk, nk_all);
+  const uint32_t kt = (nk_all + sk - 1) / sk;
+  sk = (nk_all + kt - 1) / kt;  // no empty partition
+  g.split_k = sk;
+  g.k_per_split = kt * 64;
+  q.w = (const uint32_t*)qweight;
+  q.scales = (const uint16_t*)scales;
+  q.zeros = (const uint32_t*)qzeros;
+  q.zp_const = zp_const;
+  q.group = group;
+  const size_t plane = (size_t)m * n * 4;
+  if (sk > 1) {
+    int rc = ensure_workspace(ctx, plane * sk);
+    if (rc) return rc;
+    g.y = ctx->ws;
+    g.y_split_stride = plane;
+  }
+  const dim3 grid(g.tiles_n, g.tiles_m * sk);
+  if (qzeros)
+    hipLaunchKernelGGL(w4a16_pingpong_kernel<true>, grid, dim3(512), 0, ctx->stream, q);
+  else
+    hipLaunchKernelGGL(w4a16_pingpong_kernel<false>, grid, dim3(512), 0, ctx->stream, q);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return hip_fail(e, "w4a16 ping-pong launch");
+  if (sk > 1) return launch_splitk_reduce(ctx, (const float*)ctx->ws, (void*)y, nullptr, m, n, n, sk, out_bf16, EpiChain{});
+  return T0MI_OK;
 }
 
 extern "C" int t0mi_w4a16_gemm(t0mi_ctx* ctx, uint64_t a, uint64_t qweight, uint64_t scales, uint64_t qzeros,
@@ -378,7 +439,10 @@ extern "C" int t0mi_w4a16_gemm(t0mi_ctx* ctx, uint64_t a, uint64_t qweight, uint
   p.nib_mask = 0x000F000Fu;
   p.nib_magic = 0x43004300u;
   const bool pow2_group = (group & (group - 1)) == 0;
-  if (m >= kTwoPassRows || (m > kDecodeMaxRows && !pow2_group)) {
+  const bool pingpong = w4_pingpong_ok(k, group, 1, k);
+  if (pingpong && m >= kPingPongRows && m < kTwoPassRows)
+    return launch_w4_pingpong(ctx, a, qweight, scales, qzeros, zp_const, y, m, k, n, group, p.out_bf16);
+  if (m >= (pingpong ? kTwoPassRows : kPrefillTwoPassRows) || (m > kDecodeMaxRows && !pow2_group)) {
     // W -> bf16 [K][N] (RNE of the exact (q - z) * s: the value the fused
     // kernels round to as well) in the library's conversion buffer, then the
     // NN GEMM with the cost model's config for this shape.

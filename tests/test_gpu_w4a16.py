@@ -76,10 +76,15 @@ def test_w4a16_vs_oracle(rt, m, k, n, group, pgz):
 @pytest.mark.parametrize("m,k,n,group,pgz", [
     (81, 384, 200, 128, True),       # just above the decode-slab range: 128x128 tiles, split K
     (130, 256, 136, 32, True),
-    (300, 512, 264, 64, False),      # ragged M and N tiles
+    (191, 256, 136, 128, True),      # last row count of the 128x128 fused kernel
+    (192, 256, 136, 128, True),      # first of the ping-pong fused kernel
+    (300, 512, 264, 64, False),      # ping-pong: ragged M and N tiles
+    (300, 512, 264, 32, True),       # group 32: the 128x128 fused kernel
     (200, 352, 136, 32, True),       # K % 64 == 32: the last K tile is half past K
-    (767, 256, 136, 128, True),      # last row count of the fused kernel
-    (768, 256, 136, 128, True),      # first of the two-pass route (dequant to bf16, dense GEMM)
+    (767, 256, 136, 32, True),       # group 32: last row count of the 128x128 fused kernel
+    (768, 256, 136, 32, True),       # group 32: first of the two-pass route
+    (1535, 256, 136, 128, True),     # last row count of the ping-pong kernel
+    (1536, 256, 136, 128, True),     # first of the two-pass route (dequant to bf16, dense GEMM)
     (800, 384, 264, 96, True),       # two-pass with a group that is not a power of two
     (100, 384, 136, 96, True),       # fused range, group not a power of two -> two-pass
     (1024, 1024, 512, 128, True),
@@ -87,7 +92,7 @@ def test_w4a16_vs_oracle(rt, m, k, n, group, pgz):
 ])
 def test_w4a16_prefill_vs_oracle(rt, m, k, n, group, pgz):
     """Prefill rows: the dequantised weight is rounded to bf16 (RNE), inside the K-loop
-    (fused kernel) or in a dequant pass before the dense GEMM (from 768 rows on).
+    (fused kernels) or in a dequant pass before the dense GEMM (from 1536 rows on).
     Against the oracle GEMM on RNE(exact dequant) weights the result matches to fp32
     accumulation noise (this pins the in-loop dequant bit for bit up to summation order);
     against the exact-dequant oracle it is within the GEMM tolerance."""
@@ -180,8 +185,10 @@ def test_w4a16_rejects_bad_shapes(rt):
 
 def _random_cases(n_cases=40, seed=0x5EED):
     """Seeded shapes spread over every route of t0mi_w4a16_gemm: decode slabs (1..80
-    rows), the fused kernel (81..767, power-of-two groups, with and without a K split),
-    dequant-once + dense GEMM (768+ rows, or other groups), ragged N and K."""
+    rows), the fused kernels (128x128 tiles from 81 rows, ping-pong from 192 when K and
+    the group are multiples of 64, with and without a K split), dequant-once + dense
+    GEMM (1536+ rows, 768+ for other K and groups, or groups that are not powers of
+    two), ragged N and K."""
     g = np.random.default_rng(seed)
     groups = [32, 64, 96, 128, 256, 512]
     out = []
@@ -190,7 +197,7 @@ def _random_cases(n_cases=40, seed=0x5EED):
         k = group * int(g.integers(1, max(2, 2048 // group) + 1))
         k = max(k, 32)
         n = 8 * int(g.integers(1, 160))
-        m = int(g.choice([int(g.integers(1, 81)), int(g.integers(81, 768)), int(g.integers(768, 1100))],
+        m = int(g.choice([int(g.integers(1, 81)), int(g.integers(81, 1536)), int(g.integers(1536, 1700))],
                          p=[0.45, 0.4, 0.15]))
         out.append((i, m, k, n, group, bool(g.integers(0, 2)), bool(g.integers(0, 2)), int(g.integers(0, 16))))
     return out
