@@ -359,8 +359,9 @@ static int launch_dequant(t0mi_ctx* ctx, uint64_t qweight, uint64_t scales, uint
 }
 
 // The fused ping-pong kernel (w4a16_pingpong.h): 256x256 tiles, K split so
-// that the workgroups cover the CUs when the tiles do not; partial planes are
-// summed in partition order by the split-K reduce.  Callers check
+// that the workgroups cover the CUs when the tiles do not (the split t0mi_gemm
+// would use with the same power-of-two split_k); partial planes are summed in
+// partition order by the split-K reduce.  Callers check
 // w4_pingpong_ok(k, group, ...) for whole 64-K tiles and groups.
 static int launch_w4_pingpong(t0mi_ctx* ctx, uint64_t a, uint64_t qweight, uint64_t scales, uint64_t qzeros,
                               uint32_t zp_const, uint64_t y, uint32_t m, uint32_t k, uint32_t n, uint32_t group,
@@ -379,11 +380,14 @@ static int launch_w4_pingpong(t0mi_ctx* ctx, uint64_t a, uint64_t qweight, uint6
   g.tiles_n = (n + 255) / 256;
   g.xcd_remap = 1;
   g.out_bf16 = out_bf16;
+  // A power of two (as the GEMM configs use) up to 8 and the CUs' share of
+  // tiles, halved while a partition of whole 64-K tiles would be empty.
   const uint32_t tiles = g.tiles_m * g.tiles_n, nk_all = k / 64;
-  uint32_t sk = std::max(1u, std::min(8u, (uint32_t)ctx->cu_count / std::max(1u, tiles)));
-  sk = std::min(sk, nk_all);
+  const uint32_t want = std::min(8u, (uint32_t)ctx->cu_count / std::max(1u, tiles));
+  uint32_t sk = 1;
+  while (sk * 2 <= want && sk * 2 <= nk_all) sk *= 2;
+  while (sk > 1 && ((nk_all + sk - 1) / sk) * (sk - 1) >= nk_all) sk /= 2;
   const uint32_t kt = (nk_all + sk - 1) / sk;
-  sk = (nk_all + kt - 1) / kt;  // no empty partition
   g.split_k = sk;
   g.k_per_split = kt * 64;
   q.w = (const uint32_t*)qweight;

@@ -172,3 +172,32 @@ def test_bf16_out_to_8_byte_aligned_y(rt, preset):
     raw = from_dev(dy2, np.uint8, (m * n * 2 + 16,))
     assert np.all(raw[:8] == 0xAB) and np.all(raw[8 + m * n * 2:] == 0xAB)
     assert np.array_equal(raw[8:8 + m * n * 2].view(np.uint16).reshape(m, n), aligned)
+
+
+def _random_cases(n_cases=24, seed=0x9A9A):
+    """Seeded shapes through the 256x256x64 configuration: ragged M and N, K a
+    multiple of 64 (ping-pong) or of 8 only (generic kernel), split-K 1..8, NN
+    and NT, f32 and bf16 output."""
+    g = np.random.default_rng(seed)
+    out = []
+    for i in range(n_cases):
+        m = int(g.integers(1, 700))
+        n = 8 * int(g.integers(1, 90))
+        k = 64 * int(g.integers(1, 24)) if g.random() < 0.75 else 8 * int(g.integers(1, 190))
+        sk = int(g.choice([1, 1, 2, 4, 8]))
+        layout = t0mi.NN if g.random() < 0.5 else t0mi.NT
+        out.append((i, m, n, k, sk, layout, bool(g.integers(0, 2))))
+    return out
+
+
+@pytest.mark.parametrize("i,m,n,k,sk,layout,out_bf16", _random_cases())
+def test_random_shapes(rt, i, m, n, k, sk, layout, out_bf16):
+    a = rand_bf16((m, k), 1000 + i)
+    b = rand_b(layout, n, k, 2000 + i)
+    y = run(rt, a, b, m, n, k, out_bf16, split_k=sk, layout=layout)
+    ref = oracle.gemm_bf16(a, b, lname(layout))
+    got = bf16_to_f32(y) if out_bf16 else y
+    tol = 1e-2 * np.sqrt(k) * np.abs(bf16_to_f32(a)).max() * np.abs(bf16_to_f32(b)).max()
+    assert np.abs(got - ref).max() <= tol, (i, m, n, k, sk)
+    if sk == 1 and k % 64 == 0:  # ping-pong against the generic kernel
+        assert np.array_equal(y, run_generic(rt, a, b, m, n, k, out_bf16, layout=layout)), (i, m, n, k)

@@ -45,12 +45,17 @@ def make(m, k, n, group, zeros, seed):
 
 
 def split_of(m, n, k):
-    """The split-K the W4A16 route picks: tiles of 256x256 spread over 256 CUs."""
+    """The split-K the W4A16 route picks: a power of two up to 8 and the 256 CUs'
+    share of 256x256 tiles, halved while a partition would be empty."""
     tiles = -(-m // 256) * -(-n // 256)
     nk = k // 64
-    sk = max(1, min(8, 256 // max(1, tiles), nk))
-    kt = -(-nk // sk)
-    return -(-nk // kt)
+    want = min(8, 256 // max(1, tiles))
+    sk = 1
+    while sk * 2 <= want and sk * 2 <= nk:
+        sk *= 2
+    while sk > 1 and -(-nk // sk) * (sk - 1) >= nk:
+        sk //= 2
+    return sk
 
 
 CASES = [
@@ -91,3 +96,20 @@ def test_fused_equals_two_pass_bit_for_bit(rt, m, k, n, group, zeros, out_bf16):
     got = bf16_to_f32(fused) if out_bf16 else fused
     tol = 1e-2 * np.sqrt(k) * np.abs(bf16_to_f32(a)).max() * np.abs(wf).max()
     assert np.abs(got - ref).max() <= tol
+
+
+def _random_cases(n_cases=12, seed=0x4B1D):
+    g = np.random.default_rng(seed)
+    out = []
+    for i in range(n_cases):
+        group = int(g.choice([64, 128, 256]))
+        k = group * int(g.integers(1, max(2, 2048 // group) + 1))
+        n = 8 * int(g.integers(1, 400))
+        m = int(g.integers(192, 1536))
+        out.append((i, m, k, n, group, bool(g.integers(0, 2)), bool(g.integers(0, 2))))
+    return out
+
+
+@pytest.mark.parametrize("i,m,k,n,group,zeros,out_bf16", _random_cases())
+def test_random_shapes_equal_two_pass(rt, i, m, k, n, group, zeros, out_bf16):
+    test_fused_equals_two_pass_bit_for_bit(rt, m, k, n, group, zeros, out_bf16)
