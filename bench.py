@@ -12,7 +12,8 @@ kernels are launched on (the t0mi runtime launches on torch's current stream).
 The W4A16 timing rotates over >= 512 MB of distinct weight copies so the
 256 MB Infinity Cache cannot serve repeats.
 
-Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--only gemm|w4a16] [--no-cpu]
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--only gemm|w4a16|skinny|prefill] [--no-cpu]
+       [--config PRESET] [--tune]
 """
 import argparse
 import json
@@ -33,12 +34,17 @@ def parse():
     p.add_argument("--gpus", type=int, default=1)
     p.add_argument("--steps", type=int, default=200)
     p.add_argument("--warmup", type=int, default=10)
-    p.add_argument("--only", choices=["all", "gemm", "w4a16", "copy", "dispatch"], default="all",
+    p.add_argument("--only", choices=["all", "gemm", "w4a16", "skinny", "prefill", "copy", "dispatch"],
+                   default="all",
                    help="'copy' runs only a plain 1 GiB fp32 copy kernel: the calibration for rocprofv3 "
                         "FETCH_SIZE/WRITE_SIZE readings; 'dispatch' times batched submission (a batch of "
-                        "small GEMM dispatches: synchronous, DispatchQueue, HIP graph)")
+                        "small GEMM dispatches: synchronous, DispatchQueue, HIP graph); 'skinny' and "
+                        "'prefill' time BASELINE configs 3 and 5 (parity shapes, not the headline line)")
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     p.add_argument("--config", default=None, help="GEMM preset name to force (default: auto_select)")
+    p.add_argument("--tune", action="store_true",
+                   help="with --only gemm/skinny: also run GemmTuner on the shape (fresh cache) and report "
+                        "its measured pick beside auto_select's")
     return p.parse_args()
 
 
@@ -79,6 +85,7 @@ def bench_gemm(args, torch, t0mi, rt):
     else:
         cfg = t0mi.auto_select_layout(M, K, N, t0mi.NN, t0mi.OUT_BF16)
     cfg = cfg.copy(transpose=t0mi.NN, out_dtype=t0mi.OUT_BF16)
+    args.tuned = run_tuner(t0mi, rt, M, N, K, t0mi.NN, t0mi.OUT_BF16) if args.tune else None
     pa, pb, py = a.data_ptr(), b.data_ptr(), y.data_ptr()
     warm_up(torch, lambda: rt.gemm(cfg, pa, pb, py, M, N, K), args.warmup)
     e0 = torch.cuda.Event(enable_timing=True)
@@ -96,6 +103,86 @@ def bench_gemm(args, torch, t0mi, rt):
     print(f"[bench] gemm {cfg.name()} 4096^3 NN bf16-out: {ms*1e3:.1f} us/launch, {tflops:.1f} TFLOPS "
           f"({100*tflops/PEAK_BF16_TFLOPS:.1f}% of peak); host wall {t_host:.3f}s", file=sys.stderr, flush=True)
     return cfg, ms, tflops
+
+
+def run_tuner(t0mi, rt, m, n, k, transpose, out_dtype):
+    """GemmTuner::tune on a fresh cache: the measured pick among the cost model's top
+    candidates, and the tuner's own report of every candidate it timed."""
+    import tempfile
+    with tempfile.TemporaryDirectory() as d:
+        tuner = t0mi.GemmTuner(cache_dir=d, max_candidates=8, n_iters=10)
+        cfg, tflops, _ = tuner.tune(rt, m, n, k, transpose, out_dtype)
+        report = tuner.report()
+        del tuner
+    print(f"[bench] tuner {m}x{n}x{k}: {cfg.name()} {tflops:.1f} TFLOPS\n{report}", file=sys.stderr, flush=True)
+    return {"config": cfg.name(), "tflops": round(tflops, 2)}
+
+
+def time_calls(torch, launch, calls):
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for i in range(calls):
+        launch(i)
+    e1.record()
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) * 1e3 / calls
+
+
+def bench_skinny(args, torch, t0mi, rt):
+    """Config 3: 128 x 4096 x 4096 NN, N(0, 0.02) bf16, bf16 out.  HBM-bound; B (32 MB) is
+    rotated over >= 512 MB of copies so the Infinity Cache cannot serve repeats.  One call
+    is the GEMM plus, when the chosen config splits K, its reduce."""
+    M, N, K = 128, 4096, 4096
+    copies = 16
+    g = torch.Generator(device="cuda:0")
+    g.manual_seed(0x7503)
+    a = (torch.randn(M, K, device="cuda:0", generator=g) * 0.02).to(torch.bfloat16)
+    bs = [(torch.randn(K, N, device="cuda:0", generator=g) * 0.02).to(torch.bfloat16) for _ in range(copies)]
+    y = torch.empty(M, N, device="cuda:0", dtype=torch.bfloat16)
+    cfg = t0mi.preset(args.config) if args.config else t0mi.auto_select_layout(M, K, N, t0mi.NN, t0mi.OUT_BF16)
+    cfg = cfg.copy(transpose=t0mi.NN, out_dtype=t0mi.OUT_BF16)
+    tuned = run_tuner(t0mi, rt, M, N, K, t0mi.NN, t0mi.OUT_BF16) if args.tune else None
+    pa, py = a.data_ptr(), y.data_ptr()
+
+    def launch(i):
+        rt.gemm(cfg, pa, bs[i % copies].data_ptr(), py, M, N, K)
+    rot = [0]
+
+    def launch_rot():
+        launch(rot[0])
+        rot[0] += 1
+    warm_up(torch, launch_rot, max(args.warmup, copies))
+    us = time_calls(torch, launch, max(args.steps * 4, 2 * copies))
+    alg_bytes = 2 * M * K + 2 * K * N + 2 * M * N
+    gbs = alg_bytes / (us * 1e-6) / 1e9
+    print(f"[bench] skinny {cfg.name()} 128x4096x4096 NN bf16-out: {us:.2f} us/call, {gbs:.0f} GB/s "
+          f"({100*gbs/PEAK_HBM_GBS:.1f}% of HBM peak)", file=sys.stderr, flush=True)
+    return cfg, us, gbs, alg_bytes, tuned
+
+
+def bench_prefill(args, torch, t0mi, rt):
+    """Config 5: A[4096,4096] bf16 x int4 W[4096,14336], group 128, per-group int4 zero
+    points, bf16 scales, bf16 out, through t0mi_w4a16_gemm (whichever route it takes for
+    4096 rows).  MFMA-bound."""
+    M, K, N, G = 4096, 4096, 14336, 128
+    g = torch.Generator(device="cuda:0")
+    g.manual_seed(0x7505)
+    a = torch.randn(M, K, device="cuda:0", generator=g).to(torch.bfloat16)
+    w = torch.randint(-2**31, 2**31 - 1, (K // 8, N), device="cuda:0", dtype=torch.int32, generator=g)
+    s = (torch.rand(K // G, N, device="cuda:0", generator=g) * 0.015 + 0.005).to(torch.bfloat16)
+    z = torch.randint(-2**31, 2**31 - 1, (K // G, N // 8), device="cuda:0", dtype=torch.int32, generator=g)
+    y = torch.empty(M, N, device="cuda:0", dtype=torch.bfloat16)
+    args_ = (a.data_ptr(), w.data_ptr(), s.data_ptr(), z.data_ptr(), 0, y.data_ptr(), M, K, N, G, t0mi.OUT_BF16)
+
+    def launch(i=0):
+        rt.w4a16_gemm(*args_)
+    warm_up(torch, launch, args.warmup)
+    us = time_calls(torch, launch, args.steps)
+    tflops = 2.0 * M * N * K / (us * 1e-6) / 1e12
+    print(f"[bench] prefill w4a16 4096x4096x14336 g128 zeros: {us:.1f} us/call, {tflops:.1f} TFLOPS "
+          f"({100*tflops/PEAK_BF16_TFLOPS:.1f}% of peak)", file=sys.stderr, flush=True)
+    return us, tflops
 
 
 def bench_w4a16(args, torch, t0mi, rt):
@@ -291,12 +378,40 @@ def main():
     rt = t0mi.Runtime.on_torch_stream(0)
     out = {"metric": METRIC, "n_gpus": 1, "steps": args.steps, "warmup": args.warmup, "higher_is_better": True,
            "scaling": "weak", "vs_baseline": None, "dtype": "bf16", "data": "synthetic"}
+    if args.only == "skinny":
+        cfg, us, gbs, alg_bytes, tuned = bench_skinny(args, torch, t0mi, rt)
+        out.update({"metric": "skinny bf16 GEMM HBM GB/s (% peak)", "value": round(gbs, 1), "unit": "GB/s",
+                    "ms_per_step": round(us * 1e-3, 6),
+                    "config": {"workload": "bf16 GEMM M=128, N=4096, K=4096 NN, N(0,0.02), bf16 out "
+                                           "(BASELINE config 3); one call = GEMM + split-K reduce",
+                               "kernel": cfg.name()},
+                    "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                                 "frac": round(gbs / PEAK_HBM_GBS, 4), "traffic": load_traffic("gemm_skinny")}})
+        if tuned:
+            out["tuned"] = tuned
+        rt.close()
+        print(json.dumps(out), flush=True)
+        return
+    if args.only == "prefill":
+        us, tflops = bench_prefill(args, torch, t0mi, rt)
+        out.update({"metric": "W4A16 prefill TFLOPS (% MFMA peak)", "value": round(tflops, 2), "unit": "TFLOPS",
+                    "ms_per_step": round(us * 1e-3, 6),
+                    "config": {"workload": "W4A16 A[4096,4096] bf16 x int4 W[4096,14336] g128, per-group zero "
+                                           "points, bf16 out (BASELINE config 5); one call = t0mi_w4a16_gemm"},
+                    "roofline": {"bound": "mfma", "achieved": round(tflops, 2), "peak": PEAK_BF16_TFLOPS,
+                                 "unit": "TFLOP/s", "frac": round(tflops / PEAK_BF16_TFLOPS, 4),
+                                 "traffic": load_traffic("w4a16_prefill")}})
+        rt.close()
+        print(json.dumps(out), flush=True)
+        return
     if args.only in ("all", "gemm"):
         cfg, ms, tflops = bench_gemm(args, torch, t0mi, rt)
         out.update({"value": round(tflops, 2), "unit": "TFLOPS", "ms_per_step": round(ms, 5),
                     "config": {"workload": "bf16 GEMM M=N=K=4096, A[M,K] x B[K,N] row-major (NN), N(0,1), "
                                            "fp32 accumulate, bf16 out (BASELINE config 2)",
                                "M": 4096, "N": 4096, "K": 4096, "kernel": cfg.name()}})
+        if args.tuned:
+            out["tuned"] = args.tuned
         traffic = load_traffic("gemm_4096")
         out["roofline"] = {"bound": "mfma", "achieved": round(tflops, 2), "peak": PEAK_BF16_TFLOPS,
                            "unit": "TFLOP/s", "frac": round(tflops / PEAK_BF16_TFLOPS, 4), "traffic": traffic}

@@ -287,6 +287,8 @@ extern "C" int t0mi_tuner_tune(t0mi_tuner* t, t0mi_ctx* ctx, uint32_t m, uint32_
   // 1. memory cache
   auto it = t->cache.find(key);
   if (it != t->cache.end()) {
+    fprintf(stderr, "[t0mi autotune] cache hit: %ux%ux%u -> %s (%.1f TF)\n", m, n, k,
+            config_name(it->second.best).c_str(), it->second.best_tflops);
     *best = it->second.best;
     if (tflops) *tflops = it->second.best_tflops;
     if (from_cache) *from_cache = 1;
@@ -295,6 +297,8 @@ extern "C" int t0mi_tuner_tune(t0mi_tuner* t, t0mi_ctx* ctx, uint32_t m, uint32_
   // 2. disk cache (a corrupt or stale file is ignored and re-tuned)
   TuneResult r;
   if (t->load(key, &r)) {
+    fprintf(stderr, "[t0mi autotune] cache hit: %ux%ux%u -> %s (%.1f TF)\n", m, n, k, config_name(r.best).c_str(),
+            r.best_tflops);
     t->cache[key] = r;
     *best = r.best;
     if (tflops) *tflops = r.best_tflops;
@@ -332,11 +336,13 @@ extern "C" int t0mi_tuner_tune(t0mi_tuner* t, t0mi_ctx* ctx, uint32_t m, uint32_
     return rc;
   }
   // 4. benchmark
+  fprintf(stderr, "[t0mi autotune] benchmarking %zu candidates for %ux%ux%u\n", ok_c.size(), m, n, k);
   std::vector<std::pair<t0mi_gemm_config, double>> res;
   for (const auto& c : ok_c) {
     double tf = 0;
     rc = benchmark_one(ctx, c, m, n, k, t->n_iters, &tf);
     if (rc == T0MI_OK) {
+      fprintf(stderr, "[t0mi autotune]   %s -> %.1f TFLOPS\n", config_name(c).c_str(), tf);
       res.push_back({c, tf});
     } else {
       fprintf(stderr, "[t0mi autotune]   %s -> FAILED: %s\n", config_name(c).c_str(), t0mi_last_error());
@@ -350,6 +356,7 @@ extern "C" int t0mi_tuner_tune(t0mi_tuner* t, t0mi_ctx* ctx, uint32_t m, uint32_
   r = TuneResult();
   r.best = res[0].first;
   r.best_tflops = res[0].second;
+  fprintf(stderr, "[t0mi autotune] best: %s (%.1f TFLOPS)\n", config_name(r.best).c_str(), r.best_tflops);
   for (const auto& x : res) r.all.push_back({config_name(x.first), x.second});
   // 6. persist
   t->save(key, r);
