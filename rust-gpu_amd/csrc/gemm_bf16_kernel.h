@@ -79,6 +79,8 @@ struct GemmParams {
   EpiChain epi;           // fused epilogue (final planes only)
   uint32_t swap_grid;     // reference grid axis convention (informational)
   uint32_t xcd_remap;     // 1: make tiles that share an XCD (L2) contiguous
+  uint32_t stream_out;    // 1: staged bf16 stores are non-temporal (set when all
+                          // workgroups run at once, so every store comes at the end)
 };
 
 __device__ __forceinline__ uint16_t f32_to_bf16_rne(float f) {
@@ -269,7 +271,11 @@ __device__ __forceinline__ void store_tile_bf16_staged(const GemmParams& p, cons
   for (int i = 0; i < FM * 32 / RPI; ++i) {
     const int r = i * RPI + rr;
     const u32x4 v = *(const u32x4*)(st + r * TN * 2 + ((cc ^ (r & (CH - 1))) * 16));
-    *(u32x4*)(yrow + (size_t)i * RPI * p.ldy * 2) = v;
+    u32x4* dst = (u32x4*)(yrow + (size_t)i * RPI * p.ldy * 2);
+    if (p.stream_out)
+      __builtin_nontemporal_store(v, dst);
+    else
+      *dst = v;
   }
 }
 

@@ -148,6 +148,11 @@ int launch_gemm(t0mi_ctx* ctx, const t0mi_gemm_config& cfg, const GemmLaunchEntr
   // kernel decodes the tile from the linear workgroup id either way.
   dim3 grid = cfg.swap_grid ? dim3(p.tiles_n, p.tiles_m * p.split_k) : dim3(p.tiles_m, p.tiles_n * p.split_k);
   p.swap_grid = cfg.swap_grid;
+  // With every workgroup resident from the start, all tiles finish together and
+  // the whole output is written at the end of the launch: stream it past the
+  // L2 (non-temporal) instead of leaving it dirty there (4096^3 NN: ~1% faster;
+  // with more tiles than CUs, normal stores are faster).
+  p.stream_out = nwg <= (uint32_t)ctx->cu_count;
   if (ctx->null_backend) return T0MI_OK;
   e->fn(grid, ctx->stream, p);
   hipError_t err = hipGetLastError();
