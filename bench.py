@@ -427,6 +427,7 @@ def main():
         if args.only == "w4a16":
             out.update({"value": round(gbs, 1), "unit": "GB/s", "ms_per_step": round(us * 1e-3, 6),
                         "config": {"workload": w["workload"]}})
+            out["roofline"] = out.pop("roofline_w4a16")
     if not args.no_cpu:
         try:
             if args.only in ("all", "gemm"):
