@@ -331,9 +331,10 @@ static int hip_fail(hipError_t e, const char* what) {
 }
 
 // Routes by row count (measured at K = 4096, N = 11008 and 14336):
-//  - up to kDecodeMaxRows the decode kernel runs once per 16-row slab (5 slabs
-//    cost about one launch of a fused kernel, whose dequant work per workgroup
-//    does not shrink with M);
+//  - up to kDecodeMaxRows(V2) the decode kernel runs over 16-row slabs, up to three
+//    per launch sharing one pass over the weights (16 / 32 / 48 rows: about
+//    8.4 / 10.3 / 12 us at N = 11008; a fused kernel's dequant work per
+//    workgroup does not shrink with M);
 //  - then the 128x128 fused prefill kernel (w4a16_prefill.h) up to
 //    kPingPongRows - 1 (128 rows: 40 us against 42 us for the ping-pong kernel);
 //  - then, when K and the group are multiples of 64, the fused ping-pong kernel
@@ -344,7 +345,9 @@ static int hip_fail(hipError_t e, const char* what) {
 //    dequant pass (0.5 B read + 2 B written per weight, at HBM speed) then costs
 //    less than dequantizing inside every M tile's K-loop, which is VALU work
 //    (2048 rows: 224 us two-pass against 232 us fused; 4096 rows: 414 vs 457).
-static constexpr uint32_t kDecodeMaxRows = 80;
+static constexpr uint32_t kDecodeMaxRows = 80;    // groups the one-slab decode kernels take
+static constexpr uint32_t kDecodeMaxRowsV2 = 96;  // groups 32..256: up to three slabs per launch
+                                                  // (96 rows: 26 us against 32 for the 128x128 kernel)
 static constexpr uint32_t kPingPongRows = 192;
 static constexpr uint32_t kTwoPassRows = 1536;
 static constexpr uint32_t kPrefillTwoPassRows = 768;  // groups or K the ping-pong kernel does not take
@@ -443,10 +446,12 @@ extern "C" int t0mi_w4a16_gemm(t0mi_ctx* ctx, uint64_t a, uint64_t qweight, uint
   p.nib_mask = 0x000F000Fu;
   p.nib_magic = 0x43004300u;
   const bool pow2_group = (group & (group - 1)) == 0;
+  const bool v2_group = group == 32 || group == 64 || group == 128 || group == 256;
+  const uint32_t decode_max = v2_group ? kDecodeMaxRowsV2 : kDecodeMaxRows;
   const bool pingpong = w4_pingpong_ok(k, group, 1, k);
   if (pingpong && m >= kPingPongRows && m < kTwoPassRows)
     return launch_w4_pingpong(ctx, a, qweight, scales, qzeros, zp_const, y, m, k, n, group, p.out_bf16);
-  if (m >= (pingpong ? kTwoPassRows : kPrefillTwoPassRows) || (m > kDecodeMaxRows && !pow2_group)) {
+  if (m >= (pingpong ? kTwoPassRows : kPrefillTwoPassRows) || (m > decode_max && !pow2_group)) {
     // W -> bf16 [K][N] (RNE of the exact (q - z) * s: the value the fused
     // kernels round to as well) in the library's conversion buffer, then the
     // NN GEMM with the cost model's config for this shape.
@@ -456,7 +461,7 @@ extern "C" int t0mi_w4a16_gemm(t0mi_ctx* ctx, uint64_t a, uint64_t qweight, uint
     if (rc) return rc;
     return run_gemm_auto(ctx, T0MI_NN, a, (uint64_t)ctx->cvt, y, m, n, k, out_dtype);
   }
-  if (m > kDecodeMaxRows) {  // power-of-two group here
+  if (m > decode_max) {  // power-of-two group here
     // Many rows: dequant fused into the MFMA K-loop, weights read once per tile column.
     W4PrefillParams q;
     memset(&q, 0, sizeof q);
@@ -520,9 +525,13 @@ extern "C" int t0mi_w4a16_gemm(t0mi_ctx* ctx, uint64_t a, uint64_t qweight, uint
   const uint32_t ky = (kb_tot + per_part - 1) / per_part;
   p.kb_per_split = per_part;
   const uint32_t strips = (n + 63) / 64;
-  // Row slabs of 16: the decode kernel is launched once per slab.
-  for (uint32_t r0 = 0; r0 < m; r0 += 16) {
-    const uint32_t mr = std::min(16u, m - r0);
+  // Row slabs of 16: the v2 kernel takes up to three slabs per launch (one pass
+  // over the weights feeds them all; two for group 256, whose larger chunks
+  // need twice the LDS per slab), the other kernels one.
+  const uint32_t rs_max = group == 256 ? 2 : 3;
+  for (uint32_t r0 = 0, rs = 1; r0 < m; r0 += 16 * rs) {
+    rs = v2 ? std::min(rs_max, (m - r0 + 15) / 16) : 1;
+    const uint32_t mr = std::min(16u * rs, m - r0);
     p.a = (const uint16_t*)a + (size_t)r0 * k;
     p.M = mr;
     const size_t ob = out_dtype == T0MI_OUT_BF16 ? 2 : 4;
@@ -538,13 +547,19 @@ extern "C" int t0mi_w4a16_gemm(t0mi_ctx* ctx, uint64_t a, uint64_t qweight, uint
     const bool z = qzeros != 0;
     if (v2) {
       const dim3 grid(strips, ky), block(nw2 * 64);
-#define T0MI_W4_V2(NW, G)                                                                                      \
+#define T0MI_W4_V2_RS(NW, G, RS)                                                                               \
   if (z)                                                                                                       \
-    hipLaunchKernelGGL((w4a16_decode_v2<NW, KBW2, G / 32, true, G <= 128 ? 4 : 2>), grid, block, 0,            \
+    hipLaunchKernelGGL((w4a16_decode_v2<NW, KBW2, G / 32, true, G <= 128 ? 4 : 2, RS>), grid, block, 0,        \
                        ctx->stream, p);                                                                        \
   else                                                                                                         \
-    hipLaunchKernelGGL((w4a16_decode_v2<NW, KBW2, G / 32, false, G <= 128 ? 4 : 2>), grid, block, 0,           \
+    hipLaunchKernelGGL((w4a16_decode_v2<NW, KBW2, G / 32, false, G <= 128 ? 4 : 2, RS>), grid, block, 0,       \
                        ctx->stream, p);
+#define T0MI_W4_V2(NW, G)                                                                                      \
+  switch (rs) {                                                                                                \
+    case 3: T0MI_W4_V2_RS(NW, G, (G == 256 ? 2 : 3)) break; /* never 3 for group 256 */                        \
+    case 2: T0MI_W4_V2_RS(NW, G, 2) break;                                                                     \
+    default: T0MI_W4_V2_RS(NW, G, 1) break;                                                                    \
+  }
 #define T0MI_W4_V2_G(NW)                                                                                       \
   switch (group) {                                                                                             \
     case 32: T0MI_W4_V2(NW, 32) break;                                                                         \
@@ -559,6 +574,7 @@ extern "C" int t0mi_w4a16_gemm(t0mi_ctx* ctx, uint64_t a, uint64_t qweight, uint
       }
 #undef T0MI_W4_V2_G
 #undef T0MI_W4_V2
+#undef T0MI_W4_V2_RS
     } else {
       const dim3 grid(strips, ky), block(WAVES * 64);
       if (group == 512) {

@@ -91,9 +91,14 @@ __device__ __forceinline__ float bf16f(uint32_t h) { return __builtin_bit_cast(f
 // read a clamped, valid address.  Lane (c, g) = (lane % 16, lane / 16) loads
 // the 4 words of columns n0 + 4c .. +3 for K sub-row g of each block and
 // activation row c (rows >= M read row 0 and are never stored).
-template <int NW, int KBW, int KBPG, bool ZEROS, int CH = 1>
+//
+// RS row slabs of 16 (1..3) share one pass over the weights: each dequantized
+// weight fragment feeds every slab's MFMAs, and every row goes through exactly
+// the operations of a 16-row launch on its own slab (bit-identical results).
+template <int NW, int KBW, int KBPG, bool ZEROS, int CH = 1, int RS = 1>
 __global__ __launch_bounds__(NW * 64) void w4a16_decode_v2(W4Params p) {
   static_assert(KBW % KBPG == 0, "whole groups per wave");
+  static_assert(RS >= 1 && RS <= 3, "one to three row slabs (four spill registers)");
   constexpr int NG = KBW / KBPG;
   // CH chunks per wave: chunk c's loads are issued, then its blocks computed,
   // before chunk c+1's loads (CB blocks, whole groups and pairs per chunk).
@@ -113,9 +118,11 @@ __global__ __launch_bounds__(NW * 64) void w4a16_decode_v2(W4Params p) {
   const int ngroups = kb_tot / KBPG;
   const uint32_t mask = p.nib_mask, magic = p.nib_magic;
   const bf16x8_t ones = __builtin_bit_cast(bf16x8_t, (u32x4){0x3F803F80u, 0x3F803F80u, 0x3F803F80u, 0x3F803F80u});
-  f32x4 acc[4];
+  f32x4 acc[RS][4];
 #pragma unroll
-  for (int j = 0; j < 4; ++j) acc[j] = (f32x4){0.f, 0.f, 0.f, 0.f};
+  for (int s = 0; s < RS; ++s)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) acc[s][j] = (f32x4){0.f, 0.f, 0.f, 0.f};
 
   // Activation slices are loaded 1 KB (8 rows x one 128-byte line of 64 K
   // values) per instruction, stored to LDS and read back in the MFMA layout
@@ -125,10 +132,18 @@ __global__ __launch_bounds__(NW * 64) void w4a16_decode_v2(W4Params p) {
   // so for a fixed chunk the 16 rows fall in 16 distinct 16-byte bank groups
   // and the fragment reads (16 rows x one chunk per 16 lanes) are free of bank
   // conflicts.
+  // With one slab a wave's slice keeps all its KBW blocks; with more it holds
+  // the current chunk of every slab (a chunk's LDS writes come after the
+  // previous chunk's reads have been consumed, and the slice is the wave's own).
   static_assert(KBW % 2 == 0, "k-blocks are moved in pairs");
-  constexpr int SMEM_KB = KBW > 4 ? KBW : 4;  // per wave: activations, then the reduction
+  constexpr int SMEM_KB = RS == 1 ? (KBW > 4 ? KBW : 4) : (CB > 4 ? RS * CB : RS * 4);  // KB per wave
+  static_assert(NW * SMEM_KB <= 160, "the workgroup's LDS fits a CU (160 KB)");
   __shared__ __attribute__((aligned(1024))) float smem[NW * SMEM_KB * 256];
-  const uint32_t lds_wave = lds_addr(smem) + (uint32_t)(wave * KBW * 1024);
+  const uint32_t lds_wave = lds_addr(smem) + (uint32_t)(wave * SMEM_KB * 1024);
+  // Byte offset of the 2 KB pair holding block `blk` of the chunk starting at B0, slab s.
+  auto pair_off = [](int s, int B0, int blk) {
+    return (uint32_t)((RS == 1 ? (B0 + blk) >> 1 : s * (CB / 2) + (blk >> 1)) * 2048);
+  };
   // Loads: the 16 lanes of quarter k read rows k and k+4 (two whole lines) of
   // the 8-row half; the two rows' slot sets are disjoint, so the stores are
   // conflict-free too.
@@ -149,20 +164,23 @@ __global__ __launch_bounds__(NW * 64) void w4a16_decode_v2(W4Params p) {
     constexpr bool FULL = decltype(full_c)::value;
     constexpr int B0 = decltype(chunk_c)::value * CB;  // first block of this chunk
     constexpr int G0 = B0 / KBPG, NGC = CB / KBPG;      // its groups
-    u32x4 wv[CB], at[CB];
+    u32x4 wv[CB], at[RS * CB];
     u32x2 sv[NGC];
     uint32_t zv[NGC];
     // Activation loads (L2-resident) first, then scales, weights last: loads
     // complete in issue order, so block b's dequant waits only for weight row b.
 #pragma unroll
-    for (int pp = 0; pp < CB / 2; ++pp) {
+    for (int sl = 0; sl < RS; ++sl) {
 #pragma unroll
-      for (int h = 0; h < 2; ++h) {
-        int row = 8 * h + ld_r;
-        row = row < (int)p.M ? row : 0;
-        int kofs = (kb0 + B0 + 2 * pp) * 32 + 8 * ld_x;
-        if (!FULL) kofs = kofs + 8 <= (int)p.K ? kofs : 0;
-        at[2 * pp + h] = *(const u32x4*)(p.a + (size_t)row * p.K + kofs);
+      for (int pp = 0; pp < CB / 2; ++pp) {
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+          int row = 16 * sl + 8 * h + ld_r;
+          row = row < (int)p.M ? row : 0;
+          int kofs = (kb0 + B0 + 2 * pp) * 32 + 8 * ld_x;
+          if (!FULL) kofs = kofs + 8 <= (int)p.K ? kofs : 0;
+          at[sl * CB + 2 * pp + h] = *(const u32x4*)(p.a + (size_t)row * p.K + kofs);
+        }
       }
     }
 #pragma unroll
@@ -183,25 +201,35 @@ __global__ __launch_bounds__(NW * 64) void w4a16_decode_v2(W4Params p) {
     // Activation pieces -> this wave's LDS slice (slot = lane), read back below
     // in the MFMA layout; LDS operations of one wave complete in order.
 #pragma unroll
-    for (int i = 0; i < CB; ++i)
-      *(__attribute__((address_space(3))) u32x4*)(size_t)(lds_wave + (uint32_t)(((B0 + i) >> 1) * 2048 + st_off[i & 1])) = at[i];
+    for (int sl = 0; sl < RS; ++sl)
+#pragma unroll
+      for (int i = 0; i < CB; ++i)
+        *(__attribute__((address_space(3))) u32x4*)(size_t)(lds_wave + pair_off(sl, B0, i) + (uint32_t)st_off[i & 1]) =
+            at[sl * CB + i];
 #pragma unroll
     for (int q = 0; q < NGC; ++q) {
       if (!FULL && (G0 + q) * KBPG >= nkb) break;  // wave-uniform: the ragged end of K
-      f32x4 P[4], S = {0.f, 0.f, 0.f, 0.f};
+      f32x4 P[RS][4], S[RS];
 #pragma unroll
-      for (int j = 0; j < 4; ++j) P[j] = (f32x4){0.f, 0.f, 0.f, 0.f};
+      for (int sl = 0; sl < RS; ++sl) {
+        S[sl] = (f32x4){0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int j = 0; j < 4; ++j) P[sl][j] = (f32x4){0.f, 0.f, 0.f, 0.f};
+      }
 #pragma unroll
       for (int i = 0; i < KBPG; ++i) {
         const int b = q * KBPG + i;  // block within the chunk
-        const u32x4 av = *(const __attribute__((address_space(3))) u32x4*)(size_t)(
-            lds_wave + (uint32_t)(((B0 + b) >> 1) * 2048 + rd_off[b & 1]));
-        const bf16x8_t A = perm_act(av);
-        S = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A, ones, S, 0, 0, 0);
-        P[0] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A, nib_pairs_ao(wv[b].x, mask, magic), P[0], 0, 0, 0);
-        P[1] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A, nib_pairs_ao(wv[b].y, mask, magic), P[1], 0, 0, 0);
-        P[2] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A, nib_pairs_ao(wv[b].z, mask, magic), P[2], 0, 0, 0);
-        P[3] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A, nib_pairs_ao(wv[b].w, mask, magic), P[3], 0, 0, 0);
+        const bf16x8_t W[4] = {nib_pairs_ao(wv[b].x, mask, magic), nib_pairs_ao(wv[b].y, mask, magic),
+                               nib_pairs_ao(wv[b].z, mask, magic), nib_pairs_ao(wv[b].w, mask, magic)};
+#pragma unroll
+        for (int sl = 0; sl < RS; ++sl) {
+          const u32x4 av = *(const __attribute__((address_space(3))) u32x4*)(size_t)(
+              lds_wave + pair_off(sl, B0, b) + (uint32_t)rd_off[b & 1]);
+          const bf16x8_t A = perm_act(av);
+          S[sl] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A, ones, S[sl], 0, 0, 0);
+#pragma unroll
+          for (int j = 0; j < 4; ++j) P[sl][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A, W[j], P[sl][j], 0, 0, 0);
+        }
       }
       // y += s * (P - (128 + z) * S) for the four columns ncol + j of this lane.
       const float s4[4] = {bf16f(sv[q].x & 0xFFFFu), bf16f(sv[q].x >> 16), bf16f(sv[q].y & 0xFFFFu),
@@ -209,10 +237,13 @@ __global__ __launch_bounds__(NW * 64) void w4a16_decode_v2(W4Params p) {
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
         const float z = 128.0f + (float)(ZEROS ? ((zv[q] >> (4 * ((ncol_c & 7) + j))) & 0xFu) : p.zp_const);
-        acc[j].x = fmaf(s4[j], fmaf(-z, S.x, P[j].x), acc[j].x);
-        acc[j].y = fmaf(s4[j], fmaf(-z, S.y, P[j].y), acc[j].y);
-        acc[j].z = fmaf(s4[j], fmaf(-z, S.z, P[j].z), acc[j].z);
-        acc[j].w = fmaf(s4[j], fmaf(-z, S.w, P[j].w), acc[j].w);
+#pragma unroll
+        for (int sl = 0; sl < RS; ++sl) {
+          acc[sl][j].x = fmaf(s4[j], fmaf(-z, S[sl].x, P[sl][j].x), acc[sl][j].x);
+          acc[sl][j].y = fmaf(s4[j], fmaf(-z, S[sl].y, P[sl][j].y), acc[sl][j].y);
+          acc[sl][j].z = fmaf(s4[j], fmaf(-z, S[sl].z, P[sl][j].z), acc[sl][j].z);
+          acc[sl][j].w = fmaf(s4[j], fmaf(-z, S[sl].w, P[sl][j].w), acc[sl][j].w);
+        }
       }
     }
   };
@@ -228,19 +259,23 @@ __global__ __launch_bounds__(NW * 64) void w4a16_decode_v2(W4Params p) {
   // separates the writes from the sum, in which each of 256 threads adds one
   // row segment of 4 columns over the waves (in wave order) and stores it with
   // one vector store.
-  static_assert(SMEM_KB * 256 >= 16 * 64, "a wave's slice holds its [16 x 64] partial");
+  static_assert(SMEM_KB * 256 >= RS * 16 * 64, "a wave's slice holds its [16 x 64] partials");
   float* red = smem;
   float* mine = red + wave * SMEM_KB * 256;
 #pragma unroll
-  for (int r = 0; r < 4; ++r)
-    *(f32x4*)(mine + (4 * g + r) * 64 + 4 * c) = (f32x4){acc[0][r], acc[1][r], acc[2][r], acc[3][r]};
+  for (int sl = 0; sl < RS; ++sl)
+#pragma unroll
+    for (int r = 0; r < 4; ++r)
+      *(f32x4*)(mine + sl * 1024 + (4 * g + r) * 64 + 4 * c) =
+          (f32x4){acc[sl][0][r], acc[sl][1][r], acc[sl][2][r], acc[sl][3][r]};
   __syncthreads();
-  for (int t = threadIdx.x; t < 256; t += NW * 64) {
-    const int R = t >> 4, C = t & 15;
-    f32x4 s4 = *(const f32x4*)(red + R * 64 + 4 * C);
+  for (int t = threadIdx.x; t < 256 * RS; t += NW * 64) {
+    const int C = t & 15, R = t >> 4;  // R: output row of this launch (slab R / 16)
+    const int so = (R >> 4) * 1024 + (R & 15) * 64 + 4 * C;
+    f32x4 s4 = *(const f32x4*)(red + so);
 #pragma unroll
     for (int v = 1; v < NW; ++v) {
-      const f32x4 t4 = *(const f32x4*)(red + v * SMEM_KB * 256 + R * 64 + 4 * C);
+      const f32x4 t4 = *(const f32x4*)(red + v * SMEM_KB * 256 + so);
       s4.x += t4.x;
       s4.y += t4.y;
       s4.z += t4.z;

@@ -59,7 +59,8 @@ def check(y, ref, a, wf, k, rel_max):
     (16, 8192, 256, 128, False),     # K beyond one workgroup's range -> split + reduce
     (32, 384, 200, 128, True),       # M > 16 -> several row slabs
     (76, 256, 136, 64, False),       # 5 slabs, the last one 12 rows
-    (80, 384, 200, 128, True),       # the largest row count the slabs take
+    (80, 384, 200, 128, True),       # two launches: three slabs, then two
+    (96, 384, 200, 128, True),       # the largest row count the slabs take (groups 32..256)
     (70, 384, 136, 96, True),        # slabs with a group that is not a power of two
     (3, 4096, 64, 4096, False),      # group larger than a wave's K range
 ])
@@ -74,7 +75,7 @@ def test_w4a16_vs_oracle(rt, m, k, n, group, pgz):
 
 
 @pytest.mark.parametrize("m,k,n,group,pgz", [
-    (81, 384, 200, 128, True),       # just above the decode-slab range: 128x128 tiles, split K
+    (97, 384, 200, 128, True),       # just above the decode-slab range: 128x128 tiles, split K
     (130, 256, 136, 32, True),
     (191, 256, 136, 128, True),      # last row count of the 128x128 fused kernel
     (192, 256, 136, 128, True),      # first of the ping-pong fused kernel
@@ -184,8 +185,8 @@ def test_w4a16_rejects_bad_shapes(rt):
 
 
 def _random_cases(n_cases=40, seed=0x5EED):
-    """Seeded shapes spread over every route of t0mi_w4a16_gemm: decode slabs (1..80
-    rows), the fused kernels (128x128 tiles from 81 rows, ping-pong from 192 when K and
+    """Seeded shapes spread over every route of t0mi_w4a16_gemm: decode slabs (1..96
+    rows), the fused kernels (128x128 tiles from 97 rows, 81 for other groups, ping-pong from 192 when K and
     the group are multiples of 64, with and without a K split), dequant-once + dense
     GEMM (1536+ rows, 768+ for other K and groups, or groups that are not powers of
     two), ragged N and K."""
