@@ -1,13 +1,13 @@
-"""GPU parity of the two-slab W4A16 decode launch (csrc/w4a16_decode.h, RS = 2):
-for 17..80 rows t0mi_w4a16_gemm runs the decode kernel over 32-row pairs of
-16-row slabs in one pass over the weights.  Every row goes through the
+"""GPU parity of the multi-slab W4A16 decode launch (csrc/w4a16_decode.h, RS = 2
+or 3): for 17..96 rows t0mi_w4a16_gemm runs the decode kernel over up to three
+16-row slabs per launch in one pass over the weights (two for group 256).  Every row goes through the
 operations of a 16-row launch of its own slab, so the result must be
 bit-identical to calling t0mi_w4a16_gemm on each 16-row slab separately (which
 takes the one-slab kernel), and within the GEMM tolerance of the oracle
 (w = (q - z) * s, quant_kernels.rs:24, 95-100).
-Cases: 17..80 rows (odd remainders, a trailing one-slab launch), groups 32..256
-(256: two chunks per wave), per-group and constant zero points, f32 and bf16
-output, K beyond one workgroup's range (split-K planes of 32 rows + reduce),
+Cases: 17..96 rows (odd remainders, a trailing one- or two-slab launch), groups
+32..256 (256: two chunks per wave, at most two slabs), per-group and constant zero points, f32 and bf16
+output, K beyond one workgroup's range (split-K planes of 48 rows + reduce),
 and the full decode width N = 11008.
 """
 import numpy as np
@@ -47,16 +47,18 @@ CASES = [
     (17, 512, 200, 128, True, True),
     (31, 1024, 520, 64, False, True),
     (32, 4096, 11008, 128, False, True),   # the decode shape with 32 rows
-    (33, 256, 136, 32, True, False),       # one pair, then a one-row slab
-    (48, 2048, 1000, 256, True, True),     # group 256: two chunks per wave
-    (64, 8192, 256, 128, False, False),    # K split across workgroups: 32-row planes + reduce
-    (80, 384, 200, 128, True, True),       # two pairs and a 16-row slab
+    (33, 256, 136, 32, True, False),       # three slabs, the last one row
+    (48, 2048, 1000, 256, True, True),     # group 256: two chunks per wave, two slabs then one
+    (64, 8192, 256, 128, False, False),    # K split across workgroups: 48-row planes + reduce, then 16
+    (80, 384, 200, 128, True, True),       # three slabs, then two
     (47, 512, 64, 64, False, True),
+    (48, 4096, 2048, 64, True, True),      # three slabs, 8-wave workgroups, no K split
+    (96, 4096, 520, 32, False, False),     # two three-slab launches, group 32
 ]
 
 
 @pytest.mark.parametrize("m,k,n,group,zeros,out_bf16", CASES)
-def test_two_slab_launch_equals_16_row_calls(rt, m, k, n, group, zeros, out_bf16):
+def test_multi_slab_launch_equals_16_row_calls(rt, m, k, n, group, zeros, out_bf16):
     a, w, s, z = inputs(m, k, n, group, zeros, 7 * m + k)
     da, pa = to_dev(a)
     dw, pw = to_dev(w)
