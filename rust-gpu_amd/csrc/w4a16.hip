@@ -331,12 +331,13 @@ static int hip_fail(hipError_t e, const char* what) {
 }
 
 // Routes by row count (measured at K = 4096, N = 11008 and 14336):
-//  - up to kDecodeMaxRows(V2) the decode kernel runs over 16-row slabs, up to three
-//    per launch sharing one pass over the weights (16 / 32 / 48 rows: about
-//    8.4 / 10.3 / 12 us at N = 11008; a fused kernel's dequant work per
-//    workgroup does not shrink with M);
+//  - the decode kernel over 16-row slabs, several per launch sharing one pass
+//    over the weights, for groups 32..256 up to kDecodeMaxLaunches launches
+//    (group 128: 191 rows; 16 / 32 / 48 / 64 rows in one launch: about 8.4 /
+//    10.3 / 12.9 / 15.6 us at N = 11008), for other groups up to kDecodeMaxRows
+//    rows (a fused kernel's dequant work per workgroup does not shrink with M);
 //  - then the 128x128 fused prefill kernel (w4a16_prefill.h) up to
-//    kPingPongRows - 1 (128 rows: 40 us against 42 us for the ping-pong kernel);
+//    kPingPongRows - 1 (128 rows: 34 us);
 //  - then, when K and the group are multiples of 64, the fused ping-pong kernel
 //    (w4a16_pingpong.h) below kTwoPassRows (512 rows: 81 us; the other routes
 //    98-101 us);
@@ -346,8 +347,14 @@ static int hip_fail(hipError_t e, const char* what) {
 //    less than dequantizing inside every M tile's K-loop, which is VALU work
 //    (2048 rows: 224 us two-pass against 232 us fused; 4096 rows: 414 vs 457).
 static constexpr uint32_t kDecodeMaxRows = 80;    // groups the one-slab decode kernels take
-static constexpr uint32_t kDecodeMaxRowsV2 = 96;  // groups 32..256: up to three slabs per launch
-                                                  // (96 rows: 26 us against 32 for the 128x128 kernel)
+// Groups 32..256: up to kDecodeMaxLaunches multi-slab launches (N = 11008: three
+// launches of four slabs, 191 rows, 47 us against 47 for the 128x128 kernel; two
+// launches, 96..128 rows, 26..31 us against 32..34).
+static constexpr uint32_t kDecodeMaxLaunches = 3;
+// Slabs per launch of the decode kernel: two for group 256 (whose larger chunks
+// need twice the LDS per slab), four for group 128 (the one group whose four-slab
+// registers fit without spilling), three otherwise.
+static uint32_t decode_max_slabs(uint32_t group) { return group == 256 ? 2 : group == 128 ? 4 : 3; }
 static constexpr uint32_t kPingPongRows = 192;
 static constexpr uint32_t kTwoPassRows = 1536;
 static constexpr uint32_t kPrefillTwoPassRows = 768;  // groups or K the ping-pong kernel does not take
@@ -447,7 +454,7 @@ extern "C" int t0mi_w4a16_gemm(t0mi_ctx* ctx, uint64_t a, uint64_t qweight, uint
   p.nib_magic = 0x43004300u;
   const bool pow2_group = (group & (group - 1)) == 0;
   const bool v2_group = group == 32 || group == 64 || group == 128 || group == 256;
-  const uint32_t decode_max = v2_group ? kDecodeMaxRowsV2 : kDecodeMaxRows;
+  const uint32_t decode_max = v2_group ? 16 * decode_max_slabs(group) * kDecodeMaxLaunches : kDecodeMaxRows;
   const bool pingpong = w4_pingpong_ok(k, group, 1, k);
   if (pingpong && m >= kPingPongRows && m < kTwoPassRows)
     return launch_w4_pingpong(ctx, a, qweight, scales, qzeros, zp_const, y, m, k, n, group, p.out_bf16);
@@ -525,12 +532,13 @@ extern "C" int t0mi_w4a16_gemm(t0mi_ctx* ctx, uint64_t a, uint64_t qweight, uint
   const uint32_t ky = (kb_tot + per_part - 1) / per_part;
   p.kb_per_split = per_part;
   const uint32_t strips = (n + 63) / 64;
-  // Row slabs of 16: the v2 kernel takes up to three slabs per launch (one pass
-  // over the weights feeds them all; two for group 256, whose larger chunks
-  // need twice the LDS per slab), the other kernels one.
-  const uint32_t rs_max = group == 256 ? 2 : 3;
-  for (uint32_t r0 = 0, rs = 1; r0 < m; r0 += 16 * rs) {
-    rs = v2 ? std::min(rs_max, (m - r0 + 15) / 16) : 1;
+  // Row slabs of 16: the v2 kernel takes up to decode_max_slabs(group) slabs per
+  // launch (one pass over the weights feeds them all), spread evenly over the
+  // fewest launches (5 slabs as 3 + 2, not 4 + 1); the other kernels one.
+  const uint32_t slabs = (m + 15) / 16;
+  const uint32_t launches = v2 ? (slabs + decode_max_slabs(group) - 1) / decode_max_slabs(group) : slabs;
+  for (uint32_t r0 = 0, done = 0, l = 0, rs = 1; r0 < m; r0 += 16 * rs, done += rs, ++l) {
+    rs = (slabs - done + (launches - l) - 1) / (launches - l);
     const uint32_t mr = std::min(16u * rs, m - r0);
     p.a = (const uint16_t*)a + (size_t)r0 * k;
     p.M = mr;
@@ -556,6 +564,7 @@ extern "C" int t0mi_w4a16_gemm(t0mi_ctx* ctx, uint64_t a, uint64_t qweight, uint
                        ctx->stream, p);
 #define T0MI_W4_V2(NW, G)                                                                                      \
   switch (rs) {                                                                                                \
+    case 4: T0MI_W4_V2_RS(NW, G, (G == 128 ? 4 : G == 256 ? 2 : 3)) break; /* 4 only for group 128 */         \
     case 3: T0MI_W4_V2_RS(NW, G, (G == 256 ? 2 : 3)) break; /* never 3 for group 256 */                        \
     case 2: T0MI_W4_V2_RS(NW, G, 2) break;                                                                     \
     default: T0MI_W4_V2_RS(NW, G, 1) break;                                                                    \

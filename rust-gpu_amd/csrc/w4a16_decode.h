@@ -92,13 +92,13 @@ __device__ __forceinline__ float bf16f(uint32_t h) { return __builtin_bit_cast(f
 // the 4 words of columns n0 + 4c .. +3 for K sub-row g of each block and
 // activation row c (rows >= M read row 0 and are never stored).
 //
-// RS row slabs of 16 (1..3) share one pass over the weights: each dequantized
+// RS row slabs of 16 (1..4) share one pass over the weights: each dequantized
 // weight fragment feeds every slab's MFMAs, and every row goes through exactly
 // the operations of a 16-row launch on its own slab (bit-identical results).
 template <int NW, int KBW, int KBPG, bool ZEROS, int CH = 1, int RS = 1>
 __global__ __launch_bounds__(NW * 64) void w4a16_decode_v2(W4Params p) {
   static_assert(KBW % KBPG == 0, "whole groups per wave");
-  static_assert(RS >= 1 && RS <= 3, "one to three row slabs (four spill registers)");
+  static_assert(RS >= 1 && RS <= 4, "one to four row slabs");
   constexpr int NG = KBW / KBPG;
   // CH chunks per wave: chunk c's loads are issued, then its blocks computed,
   // before chunk c+1's loads (CB blocks, whole groups and pairs per chunk).

@@ -60,7 +60,9 @@ def check(y, ref, a, wf, k, rel_max):
     (32, 384, 200, 128, True),       # M > 16 -> several row slabs
     (76, 256, 136, 64, False),       # 5 slabs, the last one 12 rows
     (80, 384, 200, 128, True),       # two launches: three slabs, then two
-    (96, 384, 200, 128, True),       # the largest row count the slabs take (groups 32..256)
+    (96, 384, 200, 128, True),       # two launches of three slabs
+    (191, 384, 200, 128, True),      # group 128: three launches of four slabs, the last decode row count
+    (144, 384, 200, 64, True),       # group 64: three launches of three slabs, the last decode row count
     (70, 384, 136, 96, True),        # slabs with a group that is not a power of two
     (3, 4096, 64, 4096, False),      # group larger than a wave's K range
 ])
@@ -75,9 +77,10 @@ def test_w4a16_vs_oracle(rt, m, k, n, group, pgz):
 
 
 @pytest.mark.parametrize("m,k,n,group,pgz", [
-    (97, 384, 200, 128, True),       # just above the decode-slab range: 128x128 tiles, split K
-    (130, 256, 136, 32, True),
-    (191, 256, 136, 128, True),      # last row count of the 128x128 fused kernel
+    (145, 384, 200, 64, True),       # group 64 just above the decode range: 128x128 tiles, split K
+    (97, 512, 200, 256, True),       # group 256 (two slabs per launch) above 96 rows: 128x128 tiles
+    (150, 256, 136, 32, True),       # group 32 above its decode range (144 rows)
+    (191, 256, 136, 64, True),       # last row count of the 128x128 fused kernel (group 64)
     (192, 256, 136, 128, True),      # first of the ping-pong fused kernel
     (300, 512, 264, 64, False),      # ping-pong: ragged M and N tiles
     (300, 512, 264, 32, True),       # group 32: the 128x128 fused kernel
@@ -185,8 +188,8 @@ def test_w4a16_rejects_bad_shapes(rt):
 
 
 def _random_cases(n_cases=40, seed=0x5EED):
-    """Seeded shapes spread over every route of t0mi_w4a16_gemm: decode slabs (1..96
-    rows), the fused kernels (128x128 tiles from 97 rows, 81 for other groups, ping-pong from 192 when K and
+    """Seeded shapes spread over every route of t0mi_w4a16_gemm: decode slabs (up to
+    191 rows by group), the fused kernels (128x128 tiles, ping-pong from 192 when K and
     the group are multiples of 64, with and without a K split), dequant-once + dense
     GEMM (1536+ rows, 768+ for other K and groups, or groups that are not powers of
     two), ragged N and K."""

@@ -1,11 +1,12 @@
 """GPU parity of the multi-slab W4A16 decode launch (csrc/w4a16_decode.h, RS = 2
-or 3): for 17..96 rows t0mi_w4a16_gemm runs the decode kernel over up to three
-16-row slabs per launch in one pass over the weights (two for group 256).  Every row goes through the
+to 4): for groups 32..256 t0mi_w4a16_gemm runs the decode kernel over up to four
+16-row slabs per launch (group 128; three for groups 32 and 64, two for 256) in
+one pass over the weights, spread evenly over the fewest launches.  Every row goes through the
 operations of a 16-row launch of its own slab, so the result must be
 bit-identical to calling t0mi_w4a16_gemm on each 16-row slab separately (which
 takes the one-slab kernel), and within the GEMM tolerance of the oracle
 (w = (q - z) * s, quant_kernels.rs:24, 95-100).
-Cases: 17..96 rows (odd remainders, a trailing one- or two-slab launch), groups
+Cases: 17..191 rows (odd remainders, a trailing one- or two-slab launch), groups
 32..256 (256: two chunks per wave, at most two slabs), per-group and constant zero points, f32 and bf16
 output, K beyond one workgroup's range (split-K planes of 48 rows + reduce),
 and the full decode width N = 11008.
@@ -54,6 +55,8 @@ CASES = [
     (47, 512, 64, 64, False, True),
     (48, 4096, 2048, 64, True, True),      # three slabs, 8-wave workgroups, no K split
     (96, 4096, 520, 32, False, False),     # two three-slab launches, group 32
+    (112, 1024, 520, 128, True, True),     # group 128: four slabs, then three
+    (191, 4096, 1000, 128, False, True),   # group 128: three four-slab launches, the last 15 rows
 ]
 
 
