@@ -382,10 +382,12 @@ int t0mi_auto_gemm(t0mi_ctx* ctx, uint64_t a, uint64_t b, uint64_t c, uint32_t m
  *  Y       [m, n] f32 or bf16 (RNE) per out_dtype.
  * Requires k % group == 0, group % 32 == 0, n % 8 == 0; A and qweight 16-byte
  * aligned, scales and Y 8-byte aligned.  Asynchronous.
- * Routes by row count: up to 96 rows (80 for groups other than 32..256) the
- * decode kernel over 16-row slabs, up to three per launch (exact dequant inside
- * the MFMA); then kernels that dequantize inside the MFMA K loop, rounding the
- * weight once to bf16: from there to 191 rows the 128x128 fused tile
+ * Routes by row count: the decode kernel over 16-row slabs (exact dequant inside
+ * the MFMA), several slabs per launch sharing one pass over the weights, in up to
+ * three launches: up to 191 rows for group 128 (four slabs per launch), 144 for
+ * groups 32 and 64, 96 for 256, 80 for other groups (one slab per launch); then
+ * kernels that dequantize inside the MFMA K loop, rounding the weight once to
+ * bf16: from there to 191 rows the 128x128 fused tile
  * kernel, 192..1535 rows (K and group multiples of 64) the 256x256 ping-pong
  * kernel, K split through the library workspace when tiles are fewer than
  * CUs; from 1536 rows (768 when K or the group is not a multiple of 64, and
