@@ -8,7 +8,7 @@ takes the one-slab kernel), and within the GEMM tolerance of the oracle
 (w = (q - z) * s, quant_kernels.rs:24, 95-100).
 Cases: 17..191 rows (odd remainders, a trailing one- or two-slab launch), groups
 32..256 (256: two chunks per wave, at most two slabs), per-group and constant zero points, f32 and bf16
-output, K beyond one workgroup's range (split-K planes of 48 rows + reduce),
+output, K beyond one workgroup's range (split-K planes of 64 rows + reduce),
 and the full decode width N = 11008.
 """
 import numpy as np
@@ -50,7 +50,7 @@ CASES = [
     (32, 4096, 11008, 128, False, True),   # the decode shape with 32 rows
     (33, 256, 136, 32, True, False),       # three slabs, the last one row
     (48, 2048, 1000, 256, True, True),     # group 256: two chunks per wave, two slabs then one
-    (64, 8192, 256, 128, False, False),    # K split across workgroups: 48-row planes + reduce, then 16
+    (64, 8192, 256, 128, False, False),    # K split across workgroups: one four-slab launch, 64-row planes + reduce
     (80, 384, 200, 128, True, True),       # three slabs, then two
     (47, 512, 64, 64, False, True),
     (48, 4096, 2048, 64, True, True),      # three slabs, 8-wave workgroups, no K split
