@@ -42,6 +42,8 @@ def parse():
                         "'prefill' time BASELINE configs 3 and 5 (parity shapes, not the headline line)")
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     p.add_argument("--config", default=None, help="GEMM preset name to force (default: auto_select)")
+    p.add_argument("--rows", type=int, default=16,
+                   help="with --only w4a16: activation rows of the decode GEMM (default 16, BASELINE config 4)")
     p.add_argument("--tune", action="store_true",
                    help="with --only gemm/skinny: also run GemmTuner on the shape (fresh cache) and report "
                         "its measured pick beside auto_select's")
@@ -186,7 +188,7 @@ def bench_prefill(args, torch, t0mi, rt):
 
 
 def bench_w4a16(args, torch, t0mi, rt):
-    Mw, Kw, Nw, G = 16, 4096, 11008, 128
+    Mw, Kw, Nw, G = args.rows, 4096, 11008, 128
     wbytes = Kw // 8 * Nw * 4
     sbytes = Kw // G * Nw * 2
     copies = max(2, -(-512 * 1024 * 1024 // (wbytes + sbytes)))
@@ -219,7 +221,7 @@ def bench_w4a16(args, torch, t0mi, rt):
     us = e0.elapsed_time(e1) * 1e3 / calls
     alg_bytes = 2 * Mw * Kw + Kw * Nw // 2 + 2 * (Kw // G) * Nw + 2 * Mw * Nw
     gbs = alg_bytes / (us * 1e-6) / 1e9
-    print(f"[bench] w4a16 decode 16x4096x11008 g128: {us:.2f} us/call, {gbs:.0f} GB/s "
+    print(f"[bench] w4a16 decode {Mw}x4096x11008 g128: {us:.2f} us/call, {gbs:.0f} GB/s "
           f"({100*gbs/PEAK_HBM_GBS:.1f}% of HBM peak), {copies} weight copies rotated", file=sys.stderr, flush=True)
     return us, gbs, alg_bytes, copies
 
@@ -420,10 +422,12 @@ def main():
         w = {"value": round(gbs, 1), "unit": "GB/s", "us_per_call": round(us, 3),
              "frac_of_peak": round(gbs / PEAK_HBM_GBS, 4), "algorithmic_bytes": alg_bytes,
              "weight_copies_rotated": copies,
-             "workload": "W4A16 decode A[16,4096] bf16 x int4 W[4096,11008] g128 zp=8, bf16 out (BASELINE config 4)"}
+             "workload": f"W4A16 decode A[{args.rows},4096] bf16 x int4 W[4096,11008] g128 zp=8, bf16 out"
+                         + (" (BASELINE config 4)" if args.rows == 16 else "")}
         out["w4a16_decode"] = w
         out["roofline_w4a16"] = {"bound": "hbm", "achieved": round(gbs, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
-                                 "frac": round(gbs / PEAK_HBM_GBS, 4), "traffic": load_traffic("w4a16_decode")}
+                                 "frac": round(gbs / PEAK_HBM_GBS, 4),
+                                 "traffic": load_traffic("w4a16_decode") if args.rows == 16 else None}
         if args.only == "w4a16":
             out.update({"value": round(gbs, 1), "unit": "GB/s", "ms_per_step": round(us * 1e-3, 6),
                         "config": {"workload": w["workload"]}})
