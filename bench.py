@@ -90,21 +90,16 @@ def bench_gemm(args, torch, t0mi, rt):
     args.tuned = run_tuner(t0mi, rt, M, N, K, t0mi.NN, t0mi.OUT_BF16) if args.tune else None
     pa, pb, py = a.data_ptr(), b.data_ptr(), y.data_ptr()
     warm_up(torch, lambda: rt.gemm(cfg, pa, pb, py, M, N, K), args.warmup)
-    e0 = torch.cuda.Event(enable_timing=True)
-    e1 = torch.cuda.Event(enable_timing=True)
     t_host0 = time.perf_counter()
-    e0.record()
-    for _ in range(args.steps):
-        rt.gemm(cfg, pa, pb, py, M, N, K)
-    e1.record()
-    torch.cuda.synchronize()
+    us, batches = timed_batches(torch, lambda i: rt.gemm(cfg, pa, pb, py, M, N, K), args.steps)
     t_host = time.perf_counter() - t_host0
-    ms = e0.elapsed_time(e1) / args.steps
+    ms = us * 1e-3
     flops = 2.0 * M * N * K
     tflops = flops / (ms * 1e-3) / 1e12
-    print(f"[bench] gemm {cfg.name()} 4096^3 NN bf16-out: {ms*1e3:.1f} us/launch, {tflops:.1f} TFLOPS "
+    print(f"[bench] gemm {cfg.name()} 4096^3 NN bf16-out: {us:.1f} us/launch (median of {len(batches)} batches "
+          f"of {args.steps}: {', '.join(f'{b:.1f}' for b in batches)}), {tflops:.1f} TFLOPS "
           f"({100*tflops/PEAK_BF16_TFLOPS:.1f}% of peak); host wall {t_host:.3f}s", file=sys.stderr, flush=True)
-    return cfg, ms, tflops
+    return cfg, ms, tflops, batches
 
 
 def run_tuner(t0mi, rt, m, n, k, transpose, out_dtype):
@@ -120,15 +115,27 @@ def run_tuner(t0mi, rt, m, n, k, transpose, out_dtype):
     return {"config": cfg.name(), "tflops": round(tflops, 2)}
 
 
-def time_calls(torch, launch, calls):
+BATCHES = 5
+
+
+def time_calls(torch, launch, calls, start=0):
+    """Microseconds per launch over `calls` back-to-back launches, from HIP events recorded
+    on torch's current stream (the stream the t0mi runtime launches on)."""
     e0 = torch.cuda.Event(enable_timing=True)
     e1 = torch.cuda.Event(enable_timing=True)
     e0.record()
     for i in range(calls):
-        launch(i)
+        launch(start + i)
     e1.record()
     torch.cuda.synchronize()
     return e0.elapsed_time(e1) * 1e3 / calls
+
+
+def timed_batches(torch, launch, calls, batches=BATCHES):
+    """The median over `batches` event-timed batches of `calls` launches each (launch(i) gets a
+    running index, so rotations continue across batches), and every batch's value."""
+    vals = [time_calls(torch, launch, calls, start=b * calls) for b in range(batches)]
+    return sorted(vals)[len(vals) // 2], vals
 
 
 def bench_skinny(args, torch, t0mi, rt):
@@ -155,10 +162,11 @@ def bench_skinny(args, torch, t0mi, rt):
         launch(rot[0])
         rot[0] += 1
     warm_up(torch, launch_rot, max(args.warmup, copies))
-    us = time_calls(torch, launch, max(args.steps * 4, 2 * copies))
+    us, batches = timed_batches(torch, launch, max(args.steps * 4, 2 * copies))
     alg_bytes = 2 * M * K + 2 * K * N + 2 * M * N
     gbs = alg_bytes / (us * 1e-6) / 1e9
-    print(f"[bench] skinny {cfg.name()} 128x4096x4096 NN bf16-out: {us:.2f} us/call, {gbs:.0f} GB/s "
+    print(f"[bench] skinny {cfg.name()} 128x4096x4096 NN bf16-out: {us:.2f} us/call (median of "
+          f"{', '.join(f'{b:.2f}' for b in batches)}), {gbs:.0f} GB/s "
           f"({100*gbs/PEAK_HBM_GBS:.1f}% of HBM peak)", file=sys.stderr, flush=True)
     return cfg, us, gbs, alg_bytes, tuned
 
@@ -180,9 +188,10 @@ def bench_prefill(args, torch, t0mi, rt):
     def launch(i=0):
         rt.w4a16_gemm(*args_)
     warm_up(torch, launch, args.warmup)
-    us = time_calls(torch, launch, args.steps)
+    us, batches = timed_batches(torch, launch, args.steps)
     tflops = 2.0 * M * N * K / (us * 1e-6) / 1e12
-    print(f"[bench] prefill w4a16 4096x4096x14336 g128 zeros: {us:.1f} us/call, {tflops:.1f} TFLOPS "
+    print(f"[bench] prefill w4a16 4096x4096x14336 g128 zeros: {us:.1f} us/call (median of "
+          f"{', '.join(f'{b:.1f}' for b in batches)}), {tflops:.1f} TFLOPS "
           f"({100*tflops/PEAK_BF16_TFLOPS:.1f}% of peak)", file=sys.stderr, flush=True)
     return us, tflops
 
@@ -209,21 +218,33 @@ def bench_w4a16(args, torch, t0mi, rt):
         rt.w4a16_gemm(a.data_ptr(), ws[j].data_ptr(), ss[j].data_ptr(), 0, 8, y.data_ptr(), Mw, Kw, Nw, G,
                       t0mi.OUT_BF16)
     warm_up(torch, launch, max(args.warmup, copies))
-    e0 = torch.cuda.Event(enable_timing=True)
-    e1 = torch.cuda.Event(enable_timing=True)
-    e0.record()
-    for i in range(calls):
-        j = i % copies
-        rt.w4a16_gemm(a.data_ptr(), ws[j].data_ptr(), ss[j].data_ptr(), 0, 8, y.data_ptr(), Mw, Kw, Nw, G,
-                      t0mi.OUT_BF16)
-    e1.record()
-    torch.cuda.synchronize()
-    us = e0.elapsed_time(e1) * 1e3 / calls
+    pa, py = a.data_ptr(), y.data_ptr()
+    wp = [(w.data_ptr(), s.data_ptr()) for w, s in zip(ws, ss)]
+
+    def launch_i(i):
+        pw, ps = wp[i % copies]
+        rt.w4a16_gemm(pa, pw, ps, 0, 8, py, Mw, Kw, Nw, G, t0mi.OUT_BF16)
+    us, batches = timed_batches(torch, launch_i, calls)
     alg_bytes = 2 * Mw * Kw + Kw * Nw // 2 + 2 * (Kw // G) * Nw + 2 * Mw * Nw
     gbs = alg_bytes / (us * 1e-6) / 1e9
-    print(f"[bench] w4a16 decode {Mw}x4096x11008 g128: {us:.2f} us/call, {gbs:.0f} GB/s "
+    print(f"[bench] w4a16 decode {Mw}x4096x11008 g128: {us:.2f} us/call (median of {len(batches)} batches of "
+          f"{calls}: {', '.join(f'{b:.2f}' for b in batches)}), {gbs:.0f} GB/s "
           f"({100*gbs/PEAK_HBM_GBS:.1f}% of HBM peak), {copies} weight copies rotated", file=sys.stderr, flush=True)
-    return us, gbs, alg_bytes, copies
+    return us, gbs, alg_bytes, copies, batches
+
+
+def cpu_model() -> str:
+    """The host CPU's model name (from /proc/cpuinfo) and its logical CPU count."""
+    name = "unknown"
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    name = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    return f"{name} ({os.cpu_count()} logical CPUs visible)"
 
 
 def cpu_baseline(which, budget_s: float = 10.0):
@@ -233,6 +254,7 @@ def cpu_baseline(which, budget_s: float = 10.0):
     import numpy as np  # noqa: F401
     import oracle  # the CPU baseline leg is the only bench code that uses the oracle
     threads = oracle.num_threads()
+    model = cpu_model()
 
     def timed(fn):
         t0 = time.perf_counter()
@@ -252,6 +274,7 @@ def cpu_baseline(which, budget_s: float = 10.0):
         oracle.gemm_bf16(a[:64], b, "nn", nthreads=1)
         one = 2.0 * 64 * N * K / (time.perf_counter() - t1) / 1e12
         return {"value": round(2.0 * M * N * K / dt / 1e12, 4), "unit": "TFLOPS", "cores": threads, "kind": "port",
+                "cpu_model": model,
                 "one_core_TFLOPS": round(one, 5),
                 "sample": f"full 4096^3 NN GEMM x{reps} ({dt:.2f} s each) with OpenMP over rows; one-core rate "
                           f"from 64 rows; sequential fp32 per output as cpu_gemm_nt_bf16 "
@@ -263,6 +286,7 @@ def cpu_baseline(which, budget_s: float = 10.0):
     dt, reps = timed(lambda: oracle.w4a16_gemm(a, w, s, None, G, 8))
     alg_bytes = 2 * Mw * Kw + Kw * Nw // 2 + 2 * (Kw // G) * Nw + 2 * Mw * Nw
     return {"value": round(alg_bytes / dt / 1e9, 3), "unit": "GB/s", "cores": threads, "kind": "port",
+            "cpu_model": model,
             "sample": f"full 16x4096x11008 decode GEMM x{reps} ({dt*1e3:.0f} ms each): exact fp32 dequant "
                       f"then the sequential-fp32 loop, OpenMP over rows"}
 
@@ -407,8 +431,10 @@ def main():
         print(json.dumps(out), flush=True)
         return
     if args.only in ("all", "gemm"):
-        cfg, ms, tflops = bench_gemm(args, torch, t0mi, rt)
+        cfg, ms, tflops, batches = bench_gemm(args, torch, t0mi, rt)
         out.update({"value": round(tflops, 2), "unit": "TFLOPS", "ms_per_step": round(ms, 5),
+                    "timing": f"median of {len(batches)} batches of {args.steps} launches (HIP events)",
+                    "batch_us": [round(b, 2) for b in batches],
                     "config": {"workload": "bf16 GEMM M=N=K=4096, A[M,K] x B[K,N] row-major (NN), N(0,1), "
                                            "fp32 accumulate, bf16 out (BASELINE config 2)",
                                "M": 4096, "N": 4096, "K": 4096, "kernel": cfg.name()}})
@@ -418,8 +444,9 @@ def main():
         out["roofline"] = {"bound": "mfma", "achieved": round(tflops, 2), "peak": PEAK_BF16_TFLOPS,
                            "unit": "TFLOP/s", "frac": round(tflops / PEAK_BF16_TFLOPS, 4), "traffic": traffic}
     if args.only in ("all", "w4a16"):
-        us, gbs, alg_bytes, copies = bench_w4a16(args, torch, t0mi, rt)
+        us, gbs, alg_bytes, copies, wb = bench_w4a16(args, torch, t0mi, rt)
         w = {"value": round(gbs, 1), "unit": "GB/s", "us_per_call": round(us, 3),
+             "batch_us": [round(b, 3) for b in wb],
              "frac_of_peak": round(gbs / PEAK_HBM_GBS, 4), "algorithmic_bytes": alg_bytes,
              "weight_copies_rotated": copies,
              "workload": f"W4A16 decode A[{args.rows},4096] bf16 x int4 W[4096,11008] g128 zp=8, bf16 out"

@@ -70,8 +70,13 @@ typedef enum { T0MI_OUT_F32 = 0, T0MI_OUT_BF16 = 1 } t0mi_out_dtype; /* new: bf1
  * uint32_t 0/1; split_k 0 or 1 means None.  The last four fields are gfx950
  * extensions with no reference counterpart; zero keeps reference behaviour
  * (f32 output, wave layout derived from wg_size, two LDS stages).
- * wg_size is the real workgroup size in threads (64-wide waves on gfx950);
- * the reference's wave32 presets with wg_size 32 are infeasible here. */
+ * wg_size is the workgroup size the config's work-item grid is counted in.
+ * A config with no gfx950 kernel of its own shape — the wave32 preset
+ * tile_16x64_k16 (wg_size 32, 16 rows), tiles that are not whole 32x32 MFMA
+ * blocks, a tile_k of 48 — runs on the prebuilt kernel covering its tile
+ * (rows and columns rounded up to 32, K steps of 16/32/64 dividing tile_k);
+ * it keeps its name, kernargs, grid and attributes, and the results do not
+ * depend on the tile. */
 typedef struct t0mi_gemm_config {
   uint32_t tile_m, tile_n, tile_k, wg_size;
   uint32_t use_lds, double_buffer;
@@ -100,8 +105,9 @@ int t0mi_gemm_variants(char* buf, size_t len);
 uint32_t t0mi_config_n_waves(const t0mi_gemm_config* cfg);
 uint32_t t0mi_config_lds_total(const t0mi_gemm_config* cfg);
 uint32_t t0mi_config_estimated_regs(const t0mi_gemm_config* cfg);
-/* gemm_gen.rs:203-213, re-derived for gfx950 limits (wave64, 512 VGPR+AGPR,
- * 160 KB LDS).  Returns 1 if feasible, 0 otherwise. */
+/* gemm_gen.rs:203-213, re-derived for gfx950: 1 if a prebuilt kernel runs the
+ * config (its own shape within the wave64 / 512 VGPR+AGPR / 160 KB LDS limits,
+ * or the kernel covering a reference tile, see above), 0 otherwise. */
 int t0mi_config_is_feasible(const t0mi_gemm_config* cfg);
 /* GemmConfig::name (gemm_gen.rs:215-235): same tags, plus "_bf16o" for bf16
  * output and "_w{M}x{N}" for a non-default wave layout.  It is the kernel
@@ -177,8 +183,10 @@ int t0mi_memset(t0mi_ctx* ctx, uint64_t dst, int value, size_t bytes);
 
 /* ensure_kernel_t0(cfg.name(), || generate(&cfg), ...) (gpu_context.rs:212-265):
  * instead of generate + compile + GpuKernel::load, look up the prebuilt gfx950
- * code object for this config (cached by name).  kernarg_size is 40, or 48 for
- * a bias epilogue.  The kernel is owned by ctx. */
+ * code object for this config (cached by name; a reference tile without a
+ * kernel of its own shape maps to the covering kernel).  kernarg_size is 40,
+ * or 48 for a bias epilogue; wg_size and lds_size are the config's.  The
+ * kernel is owned by ctx. */
 int t0mi_kernel_get(t0mi_ctx* ctx, const t0mi_gemm_config* cfg, t0mi_kernel** out);
 /* T0Kernel::lds_size / wg_size / kernarg_size (compile.rs:641-656). */
 int t0mi_kernel_attrs(const t0mi_kernel* k, uint32_t* lds_size, uint32_t* wg_size, uint32_t* kernarg_size);
@@ -329,11 +337,12 @@ int t0mi_tile_append_epilogue_args(const t0mi_tile_spec* s, uint64_t bias, float
 int t0mi_tile_compute_grid(const t0mi_tile_spec* s, uint32_t m, uint32_t n, uint32_t grid_workitems[3]);
 /* lower_gemm + T0Kernel::compile + GpuKernel::load for a TileGemm
  * (tile_ir.rs:887; compile.rs:1398): looks up the prebuilt gfx950 kernel with
- * the spec's tile_m x tile_n x tile_k.  The handle dispatches with the spec's
- * own kernarg layout and grid; M comes from the kernarg (0 = derive it from the
- * grid, padded as gemm_gen does), and a persistent spec's one-WG grid launches
- * the full tile grid (same results).  T0MI_ERR_NO_KERNEL for shapes with no
- * gfx950 kernel (tile_k 48; NN with tile_n < 64). */
+ * the spec's tile_m x tile_n x tile_k, or the one covering it (tile_k 48 as
+ * three 16-K steps; NN tiles narrower than 64 columns on the 64-column NN
+ * kernel).  The handle dispatches with the spec's own kernarg layout and grid;
+ * M comes from the kernarg (0 = derive it from the grid, padded as gemm_gen
+ * does), and a persistent spec's one-WG grid launches the full tile grid (same
+ * results).  T0MI_ERR_NO_KERNEL when no prebuilt kernel covers the tile. */
 int t0mi_tile_kernel_get(t0mi_ctx* ctx, const t0mi_tile_spec* s, t0mi_kernel** out);
 /* One-call tile GEMM: Y[m,n] = epilogue(X[m,k] . B) for the spec's transpose,
  * with the chain's arguments; split_k > 1 is reduced deterministically (the
@@ -380,8 +389,9 @@ int t0mi_auto_gemm(t0mi_ctx* ctx, uint64_t a, uint64_t b, uint64_t c, uint32_t m
  *  qzeros  u32 [k/group][n/8] (nibble e of word j = zero of column 8j+e), or 0
  *          to use the constant zp_const for every group.
  *  Y       [m, n] f32 or bf16 (RNE) per out_dtype.
- * Requires k % group == 0, group % 32 == 0, n % 8 == 0; A and qweight 16-byte
- * aligned, scales and Y 8-byte aligned.  Asynchronous.
+ * Requires k % group == 0, group % 32 == 0, n % 8 == 0; A, qweight and Y
+ * 16-byte aligned, scales 8-byte, qzeros 4-byte.  K = 0 writes Y = 0.
+ * Asynchronous.
  * Routes by row count: the decode kernel over 16-row slabs (exact dequant inside
  * the MFMA), several slabs per launch sharing one pass over the weights, in up to
  * three launches: up to 191 rows for group 128 (four slabs per launch), 144 for

@@ -160,6 +160,73 @@ bool has_variant(const t0mi_gemm_config& c) {
   return false;
 }
 
+static uint32_t round_up(uint32_t v, uint32_t m) { return (v + m - 1) / m * m; }
+
+const GemmVariant* physical_variant(uint32_t tile_m, uint32_t tile_n, uint32_t tile_k, uint32_t wg_size,
+                                    uint32_t stages, int nn, uint32_t* bk_out) {
+  // Rows and columns round up to whole 32x32 MFMA blocks (NN B tiles to 64
+  // columns, the transpose-read width); K steps of 16, 32 or 64 divide any
+  // logical tile_k that is a multiple of 16.  Among matching kernels: the
+  // logical stage count and workgroup size if one has them, else the first.
+  const uint32_t bm = round_up(tile_m, 32);
+  const uint32_t bn = nn ? std::max(64u, round_up(tile_n, 32)) : round_up(tile_n, 32);
+  const uint32_t bk = tile_k % 64 == 0 ? 64 : tile_k % 32 == 0 ? 32 : 16;
+  const GemmVariant* best = nullptr;
+  int best_score = -1;
+  for (const auto& v : gemm_variants()) {
+    if ((uint32_t)v.bm != bm || (uint32_t)v.bn != bn || (uint32_t)v.bk != bk || v.nn != nn) continue;
+    const int score = 2 * ((uint32_t)v.stages == stages) + ((uint32_t)(64 * v.wm * v.wn) == round_up(wg_size, 64));
+    if (score > best_score) best = &v, best_score = score;
+  }
+  if (best && bk_out) *bk_out = bk;
+  return best;
+}
+
+bool config_physical(const t0mi_gemm_config& c, t0mi_gemm_config* phys, std::string* why) {
+  auto fail = [&](const std::string& m) {
+    if (why) *why = m;
+    return false;
+  };
+  // A gfx950-native config runs its own kernel.
+  std::string native_why;
+  if (config_feasible(c, &native_why) && has_variant(c)) {
+    *phys = c;
+    return true;
+  }
+  // Reference shapes with no kernel of their own on 64-wide waves (the wave32
+  // tile_16x64_k16 preset, gemm_gen.rs:88-90, that bf16_matmul.rs:140-149
+  // selects for m <= 16; rows or columns that are not whole 32x32 blocks; a
+  // tile_k of 48) run on the prebuilt kernel covering the same tile.  Results
+  // do not depend on the tile, and the logical config keeps its name, grid,
+  // kernarg layout and attributes.
+  if (c.wave_m || c.wave_n) return fail(native_why.empty() ? "no prebuilt kernel for this wave layout" : native_why);
+  if (c.wg_size < 32 || c.wg_size > 1024 || c.wg_size % 32)
+    return fail("wg_size must be a multiple of 32 in [32, 1024]");
+  if (!c.tile_m || !c.tile_n || c.tile_m % 16 || c.tile_n % 16 || c.tile_m > 256 || c.tile_n > 256)
+    return fail("tile_m and tile_n must be multiples of 16 up to 256");
+  if (!c.tile_k || c.tile_k % 16 || c.tile_k > 256) return fail("tile_k must be a multiple of 16 up to 256");
+  const uint32_t sk = split_k_of(c);
+  if (!is_pow2(sk) || sk > 16) return fail("split_k must be a power of two <= 16");
+  if (c.transpose > T0MI_NN || c.epilogue > T0MI_EPI_BIAS_ADD_RELU_STORE_F32 || c.out_dtype > T0MI_OUT_BF16)
+    return fail("bad transpose, epilogue or out_dtype");
+  if (stages_of(c) < 2 || stages_of(c) > 5) return fail("stages must be 2..5");
+  uint32_t bk = 0;
+  const GemmVariant* v = physical_variant(c.tile_m, c.tile_n, c.tile_k, c.wg_size, stages_of(c),
+                                          c.transpose == T0MI_NN, &bk);
+  if (!v) return fail(native_why.empty() ? "no prebuilt gfx950 kernel covers this tile" : native_why);
+  t0mi_gemm_config p = c;
+  p.tile_m = v->bm;
+  p.tile_n = v->bn;
+  p.tile_k = bk;
+  p.wg_size = 64u * v->wm * v->wn;
+  p.wave_m = v->wm;
+  p.wave_n = v->wn;
+  p.stages = v->stages == 2 ? 0 : v->stages;
+  if (!config_feasible(p, why)) return false;
+  *phys = p;
+  return true;
+}
+
 // ------------------------------------------------------------- cost model --
 // Analytic time estimate (microseconds) on MI355X for one config.
 static double estimate_us(const t0mi_gemm_config& c, uint32_t m, uint32_t n, uint32_t k) {
@@ -354,7 +421,8 @@ extern "C" uint32_t t0mi_config_lds_total(const t0mi_gemm_config* cfg) { return 
 extern "C" uint32_t t0mi_config_estimated_regs(const t0mi_gemm_config* cfg) { return cfg ? est_regs(*cfg) : 0; }
 
 extern "C" int t0mi_config_is_feasible(const t0mi_gemm_config* cfg) {
-  return cfg && config_feasible(*cfg, nullptr) ? 1 : 0;
+  t0mi_gemm_config phys;
+  return cfg && (config_feasible(*cfg, nullptr) || config_physical(*cfg, &phys, nullptr)) ? 1 : 0;
 }
 
 extern "C" int t0mi_config_name(const t0mi_gemm_config* cfg, char* buf, size_t len) {

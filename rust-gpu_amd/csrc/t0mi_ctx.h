@@ -36,7 +36,8 @@ enum KernelKind : int { KK_GEMM_GEN = 1, KK_TILE = 2 };
 
 struct t0mi_kernel {
   int kind;
-  t0mi_gemm_config cfg;       // KK_TILE: the lowered config of `tile`
+  t0mi_gemm_config cfg;       // KK_GEMM_GEN: the caller's config; KK_TILE: the lowered config of `tile`
+  t0mi_gemm_config phys;      // the config of the prebuilt kernel that runs (== cfg unless remapped)
   t0mi_tile_spec tile;        // KK_TILE only
   t0mi::TileArgLayout lay;    // KK_TILE only
   t0mi::EpiChain chain;

@@ -18,8 +18,9 @@ uint32_t le32(const uint8_t* p) {
 }  // namespace
 
 // GptqWeight::from_bytes (quant_kernels.rs:242-286).  Where the reference
-// asserts (header < 12 bytes, truncated data, length mismatch) or divides by a
-// zero group size, this returns T0MI_ERR_INVALID with the reason.
+// asserts (header < 12 bytes, truncated data, length mismatch), divides by a
+// zero group size or drops the last nibble of an odd element count, this
+// returns T0MI_ERR_INVALID with the reason.
 extern "C" int t0mi_gptq_parse(const void* raw, size_t len, t0mi_gptq_info* out) {
   if (!raw || !out) return set_error(T0MI_ERR_INVALID, "null pointer");
   const uint8_t* b = (const uint8_t*)raw;
@@ -30,6 +31,11 @@ extern "C" int t0mi_gptq_parse(const void* raw, size_t len, t0mi_gptq_info* out)
   info.cols = le32(b + 4);
   info.group_size = le32(b + 8);
   if (info.group_size == 0) return set_error(T0MI_ERR_INVALID, "GPTQ group_size is 0");
+  // Two INT4 values per byte: an odd element count cannot be packed (the
+  // reference's rows * cols / 2 would silently drop the last nibble).
+  if (((uint64_t)info.rows * info.cols) & 1)
+    return set_error(T0MI_ERR_INVALID, "GPTQ rows * cols = %llu is odd (two INT4 values per byte)",
+                     (unsigned long long)info.rows * info.cols);
   info.n_groups = info.cols / info.group_size;
   const uint64_t n_params = (uint64_t)info.n_groups * info.rows;
   info.packed_offset = 12;

@@ -28,6 +28,16 @@ uint32_t stages_of(const t0mi_gemm_config& c);
 // All prebuilt variants (both layouts).
 const std::vector<GemmVariant>& gemm_variants();
 bool has_variant(const t0mi_gemm_config& c);
+// The prebuilt kernel that covers a logical tile: rows and columns rounded up
+// to 32 (NN columns to at least 64), a K step of 64, 32 or 16 dividing tile_k;
+// the matching variant with the given stage count and workgroup size if there
+// is one.  *bk_out = the K step.  Null if none covers it.
+const GemmVariant* physical_variant(uint32_t tile_m, uint32_t tile_n, uint32_t tile_k, uint32_t wg_size,
+                                    uint32_t stages, int nn, uint32_t* bk_out);
+// The config whose prebuilt kernel runs `c`: `c` itself when it is feasible
+// on gfx950 and prebuilt, else the covering variant (reference shapes such as
+// the wave32 tile_16x64_k16 preset).  False with the reason if none.
+bool config_physical(const t0mi_gemm_config& c, t0mi_gemm_config* phys, std::string* why);
 
 // Cost-model candidates for (m, n, k), best first: configs whose kernels are
 // prebuilt, with split-K options.  Used by auto_select and the tuner.

@@ -413,7 +413,8 @@ extern "C" int t0mi_memset(t0mi_ctx* ctx, uint64_t dst, int value, size_t bytes)
 extern "C" int t0mi_kernel_get(t0mi_ctx* ctx, const t0mi_gemm_config* cfg, t0mi_kernel** out) {
   if (!ctx || !cfg || !out) return set_error(T0MI_ERR_INVALID, "null argument");
   std::string why;
-  if (!config_feasible(*cfg, &why))
+  t0mi_gemm_config phys;
+  if (!config_physical(*cfg, &phys, &why))
     return set_error(T0MI_ERR_INVALID, "[t0mi] config '%s' infeasible on gfx950: %s", config_name(*cfg).c_str(),
                      why.c_str());
   const std::string name = config_name(*cfg);
@@ -423,11 +424,12 @@ extern "C" int t0mi_kernel_get(t0mi_ctx* ctx, const t0mi_gemm_config* cfg, t0mi_
     *out = it->second.get();
     return T0MI_OK;
   }
-  const GemmLaunchEntry* e = find_gemm_launch(*cfg);
+  const GemmLaunchEntry* e = find_gemm_launch(phys);
   if (!e) return set_error(T0MI_ERR_NO_KERNEL, "[t0mi] no prebuilt gfx950 kernel for '%s'", name.c_str());
   std::unique_ptr<t0mi_kernel> k(new t0mi_kernel());
   k->kind = KK_GEMM_GEN;
   k->cfg = *cfg;
+  k->phys = phys;
   k->name = name;
   k->kernarg_size = cfg->epilogue == T0MI_EPI_STORE_F32 ? 40u : 48u;
   k->lds_size = t0mi_config_lds_total(cfg);
@@ -607,11 +609,18 @@ static int dispatch_impl(t0mi_ctx* ctx, const t0mi_kernel* k, const uint32_t gri
   p.N = rd_u32(ka + 28);
   p.y_split_stride = rd_u32(ka + 36);
   p.bias = ka_len >= 48 ? (const float*)rd_u64(ka + 40) : nullptr;
-  p.tiles_n = c.swap_grid ? gx : gy / sk;
-  p.tiles_m = c.swap_grid ? gy / sk : gx;
+  const uint32_t grid_tn = c.swap_grid ? gx : gy / sk;
+  const uint32_t grid_tm = c.swap_grid ? gy / sk : gx;
   // gemm_gen kernargs carry no M: the grid defines it, and callers pad Y to
   // tiles_m * tile_m rows (gemm_gen.rs:299-307).
-  p.M = p.tiles_m * c.tile_m;
+  p.M = grid_tm * c.tile_m;
+  if ((uint64_t)grid_tn * c.tile_n < p.N)
+    return set_error(T0MI_ERR_INVALID, "grid (%u tiles of %u columns) does not cover N=%u", grid_tn, c.tile_n, p.N);
+  // The launched kernel's own tiles (a remapped reference tile, e.g. 16 rows on
+  // a 32-row kernel, covers the same M x N).
+  const t0mi_gemm_config& ph = k->phys;
+  p.tiles_m = (p.M + ph.tile_m - 1) / ph.tile_m;
+  p.tiles_n = (p.N + ph.tile_n - 1) / ph.tile_n;
   p.lda = p.K;
   p.ldb = c.transpose == T0MI_NN ? p.N : p.K;
   p.ldy = p.N;
@@ -625,7 +634,7 @@ static int dispatch_impl(t0mi_ctx* ctx, const t0mi_kernel* k, const uint32_t gri
   if (p.epi.n && !p.bias) return set_error(T0MI_ERR_INVALID, "bias epilogue with null bias");
   if (sk > 1 && p.y_split_stride < (uint64_t)p.M * p.N * 4u)
     return set_error(T0MI_ERR_INVALID, "y_split_stride %llu smaller than an f32 plane", (unsigned long long)p.y_split_stride);
-  return launch_gemm(ctx, c, k->gemm, p);
+  return launch_gemm(ctx, ph, k->gemm, p);
 }
 
 extern "C" int t0mi_dispatch_async(t0mi_ctx* ctx, const t0mi_kernel* k, const uint32_t grid[3], const uint8_t* ka,
@@ -718,12 +727,13 @@ extern "C" int t0mi_gemm(t0mi_ctx* ctx, const t0mi_gemm_config* cfg, uint64_t x,
   T0MI_SUBMIT_GUARD(ctx);
   if (!cfg) return set_error(T0MI_ERR_INVALID, "null config");
   std::string why;
-  if (!config_feasible(*cfg, &why))
+  t0mi_gemm_config phys;
+  if (!config_physical(*cfg, &phys, &why))
     return set_error(T0MI_ERR_INVALID, "[t0mi] config '%s' infeasible on gfx950: %s", config_name(*cfg).c_str(),
                      why.c_str());
-  const GemmLaunchEntry* e = find_gemm_launch(*cfg);
+  const GemmLaunchEntry* e = find_gemm_launch(phys);
   if (!e) return set_error(T0MI_ERR_NO_KERNEL, "[t0mi] no prebuilt gfx950 kernel for '%s'", config_name(*cfg).c_str());
-  return run_gemm(ctx, *cfg, e, x, b, y, bias, m, n, k, chain_of(cfg->epilogue));
+  return run_gemm(ctx, phys, e, x, b, y, bias, m, n, k, chain_of(cfg->epilogue));
 }
 
 int t0mi::run_gemm_auto(t0mi_ctx* ctx, uint32_t transpose, uint64_t x, uint64_t b, uint64_t y, uint32_t m, uint32_t n,
@@ -760,6 +770,7 @@ extern "C" int t0mi_tile_kernel_get(t0mi_ctx* ctx, const t0mi_tile_spec* s, t0mi
   std::unique_ptr<t0mi_kernel> k(new t0mi_kernel());
   k->kind = KK_TILE;
   k->cfg = cfg;
+  k->phys = cfg;
   k->tile = *s;
   k->lay = tile_arg_layout(*s);
   k->chain = chain;

@@ -195,28 +195,23 @@ bool tile_lower(const t0mi_tile_spec& s, t0mi_gemm_config* cfg, std::string* why
   if (!tile_valid(s, nullptr, why)) return false;
   const int nn = s.transpose == T0MI_NN;
   const int want_stages = s.triple_buffer ? 3 : 2;
-  const GemmVariant* pick = nullptr;
-  for (const auto& v : gemm_variants()) {
-    if ((uint32_t)v.bm != s.tile_m || (uint32_t)v.bn != s.tile_n || (uint32_t)v.bk != s.tile_k || v.nn != nn)
-      continue;
-    if (v.stages == want_stages) {
-      pick = &v;
-      break;
-    }
-    if (!pick) pick = &v;
-  }
+  // The kernel with the spec's tile, or the one covering it (a k48 tile runs
+  // as three 16-K steps; NN tiles narrower than 64 columns on the 64-column
+  // NN kernel); the result does not depend on the tile.
+  uint32_t bk = 0;
+  const GemmVariant* pick =
+      physical_variant(s.tile_m, s.tile_n, s.tile_k, 0, want_stages, nn, &bk);
   if (!pick) {
     if (why)
-      *why = "no gfx950 kernel for a " + std::to_string(s.tile_m) + "x" + std::to_string(s.tile_n) + " k" +
-             std::to_string(s.tile_k) + (nn ? " NN" : " NT") +
-             " tile (tile_k must be 16/32/64, tile sides multiples of 32, NN needs tile_n >= 64)";
+      *why = "no gfx950 kernel covers a " + std::to_string(s.tile_m) + "x" + std::to_string(s.tile_n) + " k" +
+             std::to_string(s.tile_k) + (nn ? " NN" : " NT") + " tile";
     return false;
   }
   t0mi_gemm_config c;
   memset(&c, 0, sizeof c);
-  c.tile_m = s.tile_m;
-  c.tile_n = s.tile_n;
-  c.tile_k = s.tile_k;
+  c.tile_m = pick->bm;
+  c.tile_n = pick->bn;
+  c.tile_k = bk;
   c.wg_size = 64u * pick->wm * pick->wn;
   c.wave_m = pick->wm;
   c.wave_n = pick->wn;

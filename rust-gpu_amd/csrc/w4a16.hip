@@ -435,10 +435,16 @@ extern "C" int t0mi_w4a16_gemm(t0mi_ctx* ctx, uint64_t a, uint64_t qweight, uint
   if (n % 8) return set_error(T0MI_ERR_INVALID, "N=%u must be a multiple of 8", n);
   if (zp_const > 15) return set_error(T0MI_ERR_INVALID, "zp_const=%u outside 0..15", zp_const);
   if (out_dtype > T0MI_OUT_BF16) return set_error(T0MI_ERR_INVALID, "bad out_dtype");
-  if ((a | qweight) & 15) return set_error(T0MI_ERR_INVALID, "A and qweight must be 16-byte aligned");
-  if ((scales & 7) || (y & 7)) return set_error(T0MI_ERR_INVALID, "scales and Y must be 8-byte aligned");
+  // The prefill routes store whole 16-byte vectors (split-K reduce, staged
+  // tiles, the dense GEMM of the two-pass route), so Y is 16-byte aligned for
+  // every route; qzeros words are read as u32.
+  if ((a | qweight | y) & 15) return set_error(T0MI_ERR_INVALID, "A, qweight and Y must be 16-byte aligned");
+  if (scales & 7) return set_error(T0MI_ERR_INVALID, "scales must be 8-byte aligned");
+  if (qzeros & 3) return set_error(T0MI_ERR_INVALID, "qzeros must be 4-byte aligned");
   if (m == 0 || n == 0) return T0MI_OK;
   if (ctx->null_backend) return T0MI_OK;
+  // An empty contraction (K = 0, which every group divides): Y = 0.
+  if (k == 0) return fill_async(ctx, (void*)y, 0, (size_t)m * n * (out_dtype == T0MI_OUT_BF16 ? 2 : 4));
   W4Params p;
   memset(&p, 0, sizeof p);
   p.a = (const uint16_t*)a;
@@ -569,6 +575,12 @@ extern "C" int t0mi_w4a16_gemm(t0mi_ctx* ctx, uint64_t a, uint64_t qweight, uint
     case 2: T0MI_W4_V2_RS(NW, G, 2) break;                                                                     \
     default: T0MI_W4_V2_RS(NW, G, 1) break;                                                                    \
   }
+      // The switch below holds the instantiated slab counts (four only for
+      // group 128, two for group 256): a launch of more slabs than the group's
+      // kernel takes would leave rows unwritten.
+      if (rs > decode_max_slabs(group))
+        return set_error(T0MI_ERR_INVALID, "internal: %u row slabs per launch for group %u (at most %u)", rs, group,
+                         decode_max_slabs(group));
 #define T0MI_W4_V2_G(NW)                                                                                       \
   switch (group) {                                                                                             \
     case 32: T0MI_W4_V2(NW, 32) break;                                                                         \

@@ -56,11 +56,14 @@ def test_reference_preset_names_unchanged():
 
 
 def test_feasibility_gfx950():
-    assert not t0mi.preset("tile_16x64_k16").is_feasible(), "wave32 preset (wg 32) cannot run on 64-wide waves"
+    # Every reference preset runs, including the wave32 tile_16x64_k16 (wg 32, 16 rows) that
+    # bf16_matmul.rs:140-149 selects for m <= 16: it keeps its name, grid and kernargs and runs
+    # on the 32x64 kernel that covers its tile.
     for n in t0mi.preset_names():
-        if n == "tile_16x64_k16":
-            continue
         assert t0mi.preset(n).is_feasible(), n
+    small = t0mi.preset("tile_16x64_k16")
+    assert small.name() == "t0_gemm_16x64_k16_ldsdb_wgp"
+    assert t0mi.compute_grid_auto(small, 17, 100) == (2 * 32, 2), "work-items: 2 column tiles x wg 32, 2 row tiles"
     big = t0mi.preset("gfx950_256x256_k64_w2x4")
     assert t0mi.lds_total(big) == 2 * (256 + 256) * 64 * 2 <= 160 * 1024
     assert not big.copy(tile_k=48).is_feasible()
@@ -169,8 +172,11 @@ def test_null_runtime_dispatch_contract():
     g, got = rt.last_dispatch()
     assert g == (grid[0], grid[1], 1) and got == ka
     assert rt.dispatch(k, (grid[0] + 1, grid[1]), ka) == t0mi.ERR_INVALID  # not a multiple of wg
+    small = rt.kernel(t0mi.preset("tile_16x64_k16"))
+    assert small.name == "t0_gemm_16x64_k16_ldsdb_wgp"
+    assert small.attrs()["wg_size"] == 32 and small.attrs()["kernarg_size"] == 40
     with pytest.raises(t0mi.T0miError):
-        rt.kernel(t0mi.preset("tile_16x64_k16"))
+        rt.kernel(t0mi.preset("tile_16x64_k16").copy(wg_size=48))
 
 
 def test_null_runtime_timeout_poisons():
@@ -204,6 +210,16 @@ def test_gemm_argument_validation():
     with pytest.raises(t0mi.T0miError):
         rt.gemm(cfg.copy(epilogue=t0mi.EPI_BIAS_ADD), 0x1000, 0x2000, 0x3000, 64, 64, 64)  # null bias
     rt.gemm(cfg, 0x1000, 0x2000, 0x3000, 64, 64, 64)  # valid: null backend computes nothing
+    # W4A16 alignment contract: A, qweight and Y 16-byte, scales 8-byte, qzeros 4-byte
+    # (checked before the null backend returns).
+    w4 = t0mi.Runtime(null=True)
+    w4.w4a16_gemm(0x1000, 0x2000, 0x3000, 0x4000, 8, 0x5000, 16, 4096, 11008, 128)
+    for bad in ((0x1008, 0x2000, 0x3000, 0x4000, 0x5000), (0x1000, 0x2000, 0x3000, 0x4000, 0x5008),
+                (0x1000, 0x2000, 0x3004, 0x4000, 0x5000), (0x1000, 0x2000, 0x3000, 0x4002, 0x5000)):
+        a_, w_, s_, z_, y_ = bad
+        with pytest.raises(t0mi.T0miError) as e:
+            w4.w4a16_gemm(a_, w_, s_, z_, 8, y_, 16, 4096, 11008, 128)
+        assert e.value.code == t0mi.ERR_INVALID and "aligned" in str(e.value)
     with pytest.raises(t0mi.T0miError) as e:
         t0mi.Runtime(null=True).w4a16_gemm(0x1000, 0x2000, 0x3000, 0, 16, 0x4000, 16, 4096, 11008, 128)
     assert e.value.code == t0mi.ERR_INVALID  # zp_const outside 0..15

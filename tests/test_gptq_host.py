@@ -60,6 +60,15 @@ def test_from_bytes_rejects_where_the_reference_panics(raw, why):
     assert e.value.code == t0mi.ERR_INVALID and why in str(e.value)
 
 
+def test_odd_element_count_is_an_error():
+    """rows * cols odd: two INT4 values per byte cannot hold it (the reference's
+    rows * cols / 2 would drop the last nibble)."""
+    raw = container(3, 5, 5, [0] * 8, [1.0] * 3, [8] * 3)
+    with pytest.raises(t0mi.T0miError) as e:
+        t0mi.GptqWeight.from_bytes(raw)
+    assert e.value.code == t0mi.ERR_INVALID and "odd" in str(e.value)
+
+
 def test_group_size_zero_is_an_error():
     with pytest.raises(t0mi.T0miError):
         t0mi.GptqWeight.from_bytes(struct.pack("<3I", 16, 16, 0) + bytes(128))

@@ -278,3 +278,78 @@ def test_random_shapes_auto_selected(rt, i, m, n, k, layout, out_bf16, sk):
         assert np.all(np.abs(yf - ref) <= tol + np.abs(ref) * 2.0**-8), cfg.name()
     else:
         _check_tol(y, ref, a, b, k)
+
+
+def _pad(x, rows, cols):
+    out = np.zeros((rows, cols), x.dtype)
+    out[:x.shape[0], :x.shape[1]] = x
+    return out
+
+
+@pytest.mark.parametrize("m", [1, 16, 17])
+def test_reference_small_m_preset_dispatch(rt, m):
+    """GemmConfig::tile_16x64_k16 (gemm_gen.rs:88-90: 16 rows, wg_size 32, wave32) is what
+    select_config picks for m <= 16 (bf16_matmul.rs:140-149).  Through kernel_get +
+    build_kernargs + compute_grid_auto + dispatch with the reference's padding contract
+    (X, WT and Y padded to whole 16 x 64 tiles, K to 16; bf16_matmul.rs:171-199): the grid
+    is in work-items of its 32-thread workgroups and defines M; results equal the oracle."""
+    cfg = t0mi.preset("tile_16x64_k16")
+    n, k = 200, 264
+    a0, b0, _, _ = oracle.seeds(16 + m)
+    a = oracle.normal_bf16((m, k), a0, 0.0, 1.0)
+    wt = oracle.normal_bf16((n, k), b0, 0.0, 1.0)
+    mp, np_, kp = -(-m // 16) * 16, -(-n // 64) * 64, -(-k // 16) * 16
+    da, pa = to_dev(_pad(a, mp, kp))
+    db, pb = to_dev(_pad(wt, np_, kp))
+    dy, py = empty_dev(mp * np_ * 4, fill=0xAB)
+    kern = rt.kernel(cfg)
+    assert kern.name == "t0_gemm_16x64_k16_ldsdb_wgp"
+    assert kern.attrs()["wg_size"] == 32
+    ka = t0mi.build_kernargs(pa, pb, py, kp, np_, mp, cfg)
+    grid = t0mi.compute_grid_auto(cfg, mp, np_)
+    assert grid == ((np_ // 64) * 32, mp // 16)
+    assert rt.dispatch(kern, grid, ka) == 0, t0mi.last_error()
+    y = from_dev(dy, np.float32, (mp, np_))
+    ref = oracle.gemm_bf16(_pad(a, mp, kp), _pad(wt, np_, kp), "nt")
+    err, rel = oracle.compare(y, ref)
+    tol = oracle.gemm_tolerance(kp, oracle.bf16_to_f32(a), oracle.bf16_to_f32(wt))
+    assert err <= tol and rel < 1e-5, (m, err, rel)
+    assert not y[m:].any() and not y[:, n:].any(), "padding rows/columns are zero products"
+
+
+@pytest.mark.parametrize("nn", [0, 1])
+@pytest.mark.parametrize("out_bf16", [False, True])
+def test_reference_small_m_preset_gemm(rt, nn, out_bf16):
+    """t0mi_gemm with tile_16x64_k16 on ragged shapes (no padding), both layouts and outputs:
+    integer pattern, bit-exact."""
+    cfg = t0mi.preset("tile_16x64_k16").copy(transpose=nn)
+    for m, n, k in ((1, 136, 264), (16, 64, 128), (17, 200, 520)):
+        a, b = int_pattern(m, k, n, nn)
+        y = run_gemm(rt, cfg, a, b, m, n, k, out_bf16=out_bf16)
+        ref = oracle.gemm_bf16(a, b, "nn" if nn else "nt")
+        if out_bf16:
+            ref = oracle.bf16_rne(ref)
+        assert np.array_equal(y, ref), (m, n, k)
+
+
+@pytest.mark.parametrize("m", [1, 16, 17])
+def test_reference_k48_tile_dispatch(rt, m):
+    """TileGemm::tile_128x128_k48 (tile_ir.rs:316) through tile_kernel + build_kernargs_m +
+    compute_grid + dispatch (run as three 16-K steps of the 128x128 kernel), and through
+    tile_gemm, against the oracle: integer pattern, bit-exact."""
+    spec = t0mi.tile_preset("tile_128x128_k48")
+    n, k = 136, 240
+    a, b = int_pattern(m, k, n, False)
+    tm = -(-m // 128) * 128
+    da, pa = to_dev(_pad(a, tm, k))
+    db, pb = to_dev(b)
+    dy, py = empty_dev(m * n * 4, fill=0xAB)
+    kern = rt.tile_kernel(spec)
+    ka = t0mi.tile_build_kernargs_m(pa, pb, py, k, n, m, spec)
+    assert len(ka) == kern.attrs()["kernarg_size"] == 44
+    assert rt.dispatch(kern, t0mi.tile_compute_grid(spec, m, n), ka) == 0, t0mi.last_error()
+    ref = oracle.gemm_bf16(a, b, "nt")
+    assert np.array_equal(from_dev(dy, np.float32, (m, n)), ref)
+    dy2, py2 = empty_dev(m * n * 4, fill=0xAB)
+    rt.tile_gemm(spec, pa, pb, py2, m, n, k)
+    assert np.array_equal(from_dev(dy2, np.float32, (m, n)), ref)

@@ -11,7 +11,7 @@ import numpy as np
 import pytest
 
 import t0mi
-from gpu_helpers import empty_dev, to_dev, torch
+from gpu_helpers import check_guard, empty_dev, to_dev, torch
 
 pytestmark = pytest.mark.gpu
 
@@ -96,7 +96,7 @@ class Batch:
 
     def reset(self, byte):
         for d, _ in self.outs.values():
-            d.fill_(byte)
+            d[:d.t0mi_guard].fill_(byte)  # the guard bytes past each buffer keep their pattern
         torch().cuda.synchronize()
 
     def run(self):
@@ -110,7 +110,9 @@ class Batch:
 
     def results(self):
         torch().cuda.synchronize()
-        return {k: d.cpu().numpy().copy() for k, (d, _) in self.outs.items()}
+        for d, _ in self.outs.values():
+            check_guard(d)
+        return {k: d[:d.t0mi_guard].cpu().numpy().copy() for k, (d, _) in self.outs.items()}
 
 
 def test_graph_replays_match_eager(rt):

@@ -16,7 +16,7 @@ from gpu_helpers import empty_dev, from_dev, runtime, to_dev
 
 pytestmark = pytest.mark.gpu
 
-PRESETS = [p for p in t0mi.tile_preset_names() if p != "tile_128x128_k48"]
+PRESETS = t0mi.tile_preset_names()
 
 
 @pytest.fixture(scope="module")
@@ -48,9 +48,8 @@ def run_tile(rt, spec, a, b, m, n, k, bias=None, scale=1.0, lo=0.0, hi=0.0):
 @pytest.mark.parametrize("preset", PRESETS)
 @pytest.mark.parametrize("nn", [0, 1])
 def test_presets_integer_exact(rt, preset, nn):
+    # NN tiles narrower than 64 columns run on the 64-column NN kernel; tile_k 48 as three 16-K steps.
     spec = t0mi.tile_preset(preset).copy(transpose=nn)
-    if nn and spec.tile_n < 64:
-        pytest.skip("NN tiles need tile_n >= 64 on gfx950 (no kernel; rejected with T0MI_ERR_NO_KERNEL)")
     m, n, k = 200, 136, 264
     a, b = int_pattern(m, k, n, nn)
     y = run_tile(rt, spec, a, b, m, n, k)
@@ -180,7 +179,7 @@ def test_auto_selected_spec_runs(rt):
     assert np.array_equal(y, oracle.gemm_bf16(a, b, "nn"))
 
 
-def test_rejects_k48(rt):
+def test_rejects_tile_without_kernel(rt):
     with pytest.raises(t0mi.T0miError) as e:
-        rt.tile_gemm(t0mi.tile_preset("tile_128x128_k48"), 0, 0, 0, 128, 128, 128)
+        rt.tile_gemm(t0mi.tile_preset("tile_128x128_k48").copy(tile_m=512), 0, 0, 0, 128, 128, 128)
     assert e.value.code == -2

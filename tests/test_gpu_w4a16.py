@@ -178,6 +178,44 @@ def test_dequant_bit_exact(rt, round_mode, pgz, k, n, group):
         assert np.array_equal(got, want)
 
 
+@pytest.mark.parametrize("m", [16, 200, 800])
+@pytest.mark.parametrize("out_bf16", [False, True])
+def test_w4a16_k0_writes_zeros(rt, m, out_bf16):
+    """K = 0 (every group divides it): the empty contraction is Y = 0 on every route
+    (decode, fused, dequant-once row counts), not a division by zero or a stale Y."""
+    n = 264
+    ob = 2 if out_bf16 else 4
+    dy, py = empty_dev(m * n * ob, fill=0xCD)
+    da, pa = to_dev(np.zeros(16, np.uint16))
+    dw, pw = to_dev(np.zeros(16, np.uint32))
+    ds, ps = to_dev(np.zeros(16, np.uint16))
+    rt.w4a16_gemm(pa, pw, ps, 0, 8, py, m, 0, n, 128, t0mi.OUT_BF16 if out_bf16 else t0mi.OUT_F32)
+    y = from_dev(dy, np.uint8, (m * n * ob,))
+    assert not y.any()
+
+
+@pytest.mark.parametrize("m", [16, 200, 1600])
+def test_w4a16_y_alignment_contract(rt, m):
+    """Y must be 16-byte aligned on every route (the prefill routes store 16-byte
+    vectors); an 8-byte offset is refused before anything runs, a 16-byte offset works."""
+    k, n, group = 256, 136, 128
+    a, q, w, s, z = make_case(m, k, n, group, True, seed=0xA0)
+    da, pa = to_dev(a)
+    dw, pw = to_dev(w)
+    ds, ps = to_dev(s)
+    dz, pz = to_dev(z)
+    dy, py = empty_dev(m * n * 2 + 16, fill=0xCD)
+    with pytest.raises(t0mi.T0miError) as e:
+        rt.w4a16_gemm(pa, pw, ps, pz, 8, py + 8, m, k, n, group, t0mi.OUT_BF16)
+    assert e.value.code == t0mi.ERR_INVALID and "16-byte" in str(e.value)
+    rt.w4a16_gemm(pa, pw, ps, pz, 8, py + 16, m, k, n, group, t0mi.OUT_BF16)
+    raw = from_dev(dy, np.uint8, (m * n * 2 + 16,))
+    assert (raw[:16] == 0xCD).all()
+    y = oracle.bf16_to_f32(raw[16:].view(np.uint16).reshape(m, n).copy())
+    wf = oracle.dequant_qweight_f32(w, s, z, group, 8)
+    check(y, oracle.w4a16_gemm(a, w, s, z, group, 8), a, wf, k, 6e-3)
+
+
 def test_w4a16_rejects_bad_shapes(rt):
     with pytest.raises(t0mi.T0miError):
         rt.w4a16_gemm(16, 16, 16, 0, 8, 16, 16, 4096, 100, 128)   # N % 8 != 0
