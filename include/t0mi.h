@@ -212,6 +212,23 @@ int t0mi_wait_idle(t0mi_ctx* ctx);
 int t0mi_gemm(t0mi_ctx* ctx, const t0mi_gemm_config* cfg, uint64_t x, uint64_t b, uint64_t y,
               uint64_t bias, uint32_t m, uint32_t n, uint32_t k);
 
+/* Bytes of the per-GPU scratch array behind t0mi_gemm_noalloc. */
+#define T0MI_NOALLOC_SCRATCH_BYTES (32u << 20)
+/* No counterpart in the reference.  For callers that cannot allocate device
+ * memory (code under HIP graph capture, tight serving loops, harnesses that
+ * forbid hipMalloc): t0mi_gemm with the same arguments, kernels and results,
+ * except that its split-K partial planes (and the zero plane of K = 0) live
+ * in a static array of T0MI_NOALLOC_SCRATCH_BYTES bytes that every GPU the
+ * library runs on holds until the process ends, instead of the runtime's
+ * growable workspace.  It calls no hipMalloc or hipFree.  A call needing more
+ * than that (M * N * 4 * split_k bytes; M * N * 4 when K = 0) fails with
+ * T0MI_ERR_INVALID before anything is launched.  Every runtime on one GPU
+ * shares that GPU's array: calls that overlap on one GPU (two streams or two
+ * runtimes) race; calls on one stream are ordered.  Nothing in the array needs
+ * to start at zero.  Asynchronous. */
+int t0mi_gemm_noalloc(t0mi_ctx* ctx, const t0mi_gemm_config* cfg, uint64_t x, uint64_t b, uint64_t y,
+                      uint64_t bias, uint32_t m, uint32_t n, uint32_t k);
+
 /* ---- batched submission: DispatchQueue (src/t0/prefill_dispatch.rs:58-214) - */
 typedef struct t0mi_dispatch_queue t0mi_dispatch_queue;
 /* DispatchQueue::new (prefill_dispatch.rs:73-79). */

@@ -67,6 +67,12 @@ struct t0mi_ctx {
   // from ws, which the GEMMs they launch may use for split-K).
   void* cvt = nullptr;
   size_t cvt_bytes = 0;
+  // This device's copy of the library's static scratch array (device
+  // address, looked up once per device when the first runtime on it is
+  // created) and the error of that lookup if it failed.  Used only by
+  // t0mi_gemm_noalloc; shared by every runtime on the device.
+  void* scratch = nullptr;
+  int scratch_rc = 0;
   // Instantiated graphs captured on this runtime: their kernel nodes hold ws
   // and cvt addresses, so neither buffer may move while one is alive.
   std::atomic<int> live_graphs{0};
@@ -107,6 +113,13 @@ int launch_splitk_reduce(t0mi_ctx* ctx, const float* ws, void* y, const float* b
 EpiChain chain_of(uint32_t gemm_gen_epilogue);
 // Y[m,n] = epi(X . B) with a prebuilt kernel: tile-aligned or not, split-K
 // through the workspace and a deterministic reduce.  Asynchronous.
+// A fixed workspace handed to run_gemm in place of ctx->ws: never grown; a
+// GEMM that needs more than `cap` bytes of it is refused before any launch.
+struct FixedWorkspace {
+  void* ptr;
+  size_t cap;
+};
 int run_gemm(t0mi_ctx* ctx, const t0mi_gemm_config& cfg, const GemmLaunchEntry* e, uint64_t x, uint64_t b,
-             uint64_t y, uint64_t bias, uint32_t m, uint32_t n, uint32_t k, const EpiChain& epi);
+             uint64_t y, uint64_t bias, uint32_t m, uint32_t n, uint32_t k, const EpiChain& epi,
+             const FixedWorkspace* fixed = nullptr);
 }  // namespace t0mi

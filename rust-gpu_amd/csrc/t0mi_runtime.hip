@@ -250,6 +250,34 @@ int launch_splitk_reduce(t0mi_ctx* ctx, const float* ws, void* y, const float* b
 }
 }  // namespace t0mi
 
+// ------------------------------------------- scratch of t0mi_gemm_noalloc ----
+
+// Split-K partial planes of t0mi_gemm_noalloc.  Every GPU the library runs on
+// holds its own copy until the process ends.  In host code `scratch` names a
+// host-side stand-in: only the address hipGetSymbolAddress returns for a
+// device may reach a kernel or a copy.
+static __device__ __align__(256) uint8_t scratch[T0MI_NOALLOC_SCRATCH_BYTES];
+
+// This device's address of `scratch`, looked up once per device with that
+// device current (the caller has made it current).
+static int scratch_for_device(int dev, void** out) {
+  static std::mutex mu;
+  static std::map<int, std::pair<void*, hipError_t>> known;
+  std::lock_guard<std::mutex> lock(mu);
+  auto it = known.find(dev);
+  if (it == known.end()) {
+    void* ptr = nullptr;
+    hipError_t e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (e != hipSuccess) ptr = nullptr;
+    it = known.emplace(dev, std::make_pair(ptr, e)).first;
+  }
+  *out = it->second.first;
+  if (it->second.second != hipSuccess)
+    return set_error(T0MI_ERR_HIP, "hipGetSymbolAddress(scratch) on device %d: %s", dev,
+                     hipGetErrorString(it->second.second));
+  return T0MI_OK;
+}
+
 // ===================================================================== C ABI ==
 
 static int ctx_create(int device, bool use_given_stream, void* hip_stream, t0mi_ctx** out) {
@@ -292,6 +320,8 @@ static int ctx_create(int device, bool use_given_stream, void* hip_stream, t0mi_
     }
     c->own_stream = true;
   }
+  // A failed lookup leaves the runtime usable; only t0mi_gemm_noalloc reports it.
+  c->scratch_rc = scratch_for_device(dev, &c->scratch);
   *out = c;
   return T0MI_OK;
 }
@@ -662,7 +692,8 @@ extern "C" int t0mi_wait_idle(t0mi_ctx* ctx) {
 
 namespace t0mi {
 int run_gemm(t0mi_ctx* ctx, const t0mi_gemm_config& cfg, const GemmLaunchEntry* e, uint64_t x, uint64_t b,
-             uint64_t y, uint64_t bias, uint32_t m, uint32_t n, uint32_t k, const EpiChain& epi) {
+             uint64_t y, uint64_t bias, uint32_t m, uint32_t n, uint32_t k, const EpiChain& epi,
+             const FixedWorkspace* fixed) {
   if (m == 0 || n == 0) return T0MI_OK;
   if (k % 8) return set_error(T0MI_ERR_INVALID, "K=%u must be a multiple of 8", k);
   if (n % 8) return set_error(T0MI_ERR_INVALID, "N=%u must be a multiple of 8", n);
@@ -687,16 +718,31 @@ int run_gemm(t0mi_ctx* ctx, const t0mi_gemm_config& cfg, const GemmLaunchEntry* 
   p.epi = epi;
   p.out_bf16 = cfg.out_dtype == T0MI_OUT_BF16;
   p.xcd_remap = 1;
+  const size_t plane = (size_t)m * n * 4;
+  // The f32 workspace this call needs: none, one zero plane (K = 0) or one
+  // plane per K partition.  A fixed workspace is checked before any launch.
+  const size_t ws_need = k == 0 ? plane : sk > 1 ? plane * sk : 0;
+  if (fixed && ws_need > fixed->cap)
+    return set_error(T0MI_ERR_INVALID,
+                     "%ux%u with split_k=%u needs %zu bytes of scratch; the fixed workspace holds %zu", m, n,
+                     k == 0 ? 1u : sk, ws_need, fixed->cap);
+  void* ws = nullptr;
+  if (ws_need) {
+    if (fixed) {
+      ws = fixed->ptr;
+    } else {
+      int rc = ensure_workspace(ctx, ws_need);
+      if (rc) return rc;
+      ws = ctx->ws;
+    }
+  }
   int rc;
   if (k == 0) {
     // Empty contraction: the sum is zero (plus epilogue).
     if (ctx->null_backend) return T0MI_OK;
-    rc = ensure_workspace(ctx, (size_t)m * n * 4);
+    rc = fill_async(ctx, ws, 0, plane);
     if (rc) return rc;
-    rc = fill_async(ctx, ctx->ws, 0, (size_t)m * n * 4);
-    if (rc) return rc;
-    return launch_splitk_reduce(ctx, (const float*)ctx->ws, (void*)y, (const float*)bias, m, n, n, 1u, p.out_bf16,
-                                epi);
+    return launch_splitk_reduce(ctx, (const float*)ws, (void*)y, (const float*)bias, m, n, n, 1u, p.out_bf16, epi);
   }
   if (sk == 1) {
     p.k_per_split = k;
@@ -707,16 +753,12 @@ int run_gemm(t0mi_ctx* ctx, const t0mi_gemm_config& cfg, const GemmLaunchEntry* 
   // then a reduce pass sums them in partition order.
   const uint32_t kt = (k + cfg.tile_k - 1) / cfg.tile_k;
   p.k_per_split = ((kt + sk - 1) / sk) * cfg.tile_k;
-  const size_t plane = (size_t)m * n * 4;
-  rc = ensure_workspace(ctx, plane * sk);
-  if (rc) return rc;
-  p.y = ctx->ws;
+  p.y = ws;
   p.ldy = n;
   p.y_split_stride = plane;
   rc = launch_gemm(ctx, cfg, e, p);
   if (rc || ctx->null_backend) return rc;
-  return launch_splitk_reduce(ctx, (const float*)ctx->ws, (void*)y, (const float*)bias, m, n, n, sk, p.out_bf16,
-                              epi);
+  return launch_splitk_reduce(ctx, (const float*)ws, (void*)y, (const float*)bias, m, n, n, sk, p.out_bf16, epi);
 }
 }  // namespace t0mi
 
@@ -734,6 +776,26 @@ extern "C" int t0mi_gemm(t0mi_ctx* ctx, const t0mi_gemm_config* cfg, uint64_t x,
   const GemmLaunchEntry* e = find_gemm_launch(phys);
   if (!e) return set_error(T0MI_ERR_NO_KERNEL, "[t0mi] no prebuilt gfx950 kernel for '%s'", config_name(*cfg).c_str());
   return run_gemm(ctx, phys, e, x, b, y, bias, m, n, k, chain_of(cfg->epilogue));
+}
+
+extern "C" int t0mi_gemm_noalloc(t0mi_ctx* ctx, const t0mi_gemm_config* cfg, uint64_t x, uint64_t b, uint64_t y,
+                                 uint64_t bias, uint32_t m, uint32_t n, uint32_t k) {
+  int rc = check_ctx(ctx);
+  if (rc) return rc;
+  T0MI_SUBMIT_GUARD(ctx);
+  if (!cfg) return set_error(T0MI_ERR_INVALID, "null config");
+  if (!ctx->null_backend && ctx->scratch_rc)
+    return set_error(ctx->scratch_rc, "t0mi_gemm_noalloc: the library scratch of device %d is unavailable",
+                     ctx->device);
+  std::string why;
+  t0mi_gemm_config phys;
+  if (!config_physical(*cfg, &phys, &why))
+    return set_error(T0MI_ERR_INVALID, "[t0mi] config '%s' infeasible on gfx950: %s", config_name(*cfg).c_str(),
+                     why.c_str());
+  const GemmLaunchEntry* e = find_gemm_launch(phys);
+  if (!e) return set_error(T0MI_ERR_NO_KERNEL, "[t0mi] no prebuilt gfx950 kernel for '%s'", config_name(*cfg).c_str());
+  const FixedWorkspace fixed{ctx->scratch, (size_t)T0MI_NOALLOC_SCRATCH_BYTES};
+  return run_gemm(ctx, phys, e, x, b, y, bias, m, n, k, chain_of(cfg->epilogue), &fixed);
 }
 
 int t0mi::run_gemm_auto(t0mi_ctx* ctx, uint32_t transpose, uint64_t x, uint64_t b, uint64_t y, uint32_t m, uint32_t n,

@@ -27,6 +27,7 @@ ERR_CAPTURE = -9
 NT, NN = 0, 1
 EPI_STORE_F32, EPI_BIAS_ADD, EPI_BIAS_ADD_RELU = 0, 1, 2
 OUT_F32, OUT_BF16 = 0, 1
+NOALLOC_SCRATCH_BYTES = 32 << 20  # T0MI_NOALLOC_SCRATCH_BYTES
 
 
 def build(jobs: int = 8) -> str:
@@ -186,6 +187,7 @@ SIGNATURES = {
     "t0mi_dispatch_async": (_I, [_P, _P, ctypes.POINTER(_U32), _P, _SZ]),
     "t0mi_wait_idle": (_I, [_P]),
     "t0mi_gemm": (_I, [_P, _CFG, _U64, _U64, _U64, _U64, _U32, _U32, _U32]),
+    "t0mi_gemm_noalloc": (_I, [_P, _CFG, _U64, _U64, _U64, _U64, _U32, _U32, _U32]),
     "t0mi_dq_new": (_I, [_P, ctypes.POINTER(_P)]),
     "t0mi_dq_submit": (_I, [_P, _P, ctypes.POINTER(_U32), _P, _SZ]),
     "t0mi_dq_flush": (_I, [_P, ctypes.POINTER(_SZ)]),
@@ -643,6 +645,12 @@ class Runtime:
 
     def gemm(self, cfg: GemmConfig, x: int, b: int, y: int, m: int, n: int, k: int, bias: int = 0) -> None:
         check(lib().t0mi_gemm(self.handle, ctypes.byref(cfg), x, b, y, bias, m, n, k))
+
+    def gemm_noalloc(self, cfg: GemmConfig, x: int, b: int, y: int, m: int, n: int, k: int,
+                     bias: int = 0) -> None:
+        """gemm() with its split-K planes in the library's static per-GPU scratch
+        (NOALLOC_SCRATCH_BYTES): allocates nothing; overlapping calls on one GPU race."""
+        check(lib().t0mi_gemm_noalloc(self.handle, ctypes.byref(cfg), x, b, y, bias, m, n, k))
 
     def w4a16_gemm(self, a: int, qweight: int, scales: int, qzeros: int, zp_const: int, y: int,
                    m: int, k: int, n: int, group: int, out_dtype: int = OUT_BF16) -> None:

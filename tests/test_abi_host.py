@@ -210,6 +210,17 @@ def test_gemm_argument_validation():
     with pytest.raises(t0mi.T0miError):
         rt.gemm(cfg.copy(epilogue=t0mi.EPI_BIAS_ADD), 0x1000, 0x2000, 0x3000, 64, 64, 64)  # null bias
     rt.gemm(cfg, 0x1000, 0x2000, 0x3000, 64, 64, 64)  # valid: null backend computes nothing
+    # the no-allocation variant: same checks, plus the scratch limit (checked before any launch)
+    text = open(os.path.join(ROOT, "include", "t0mi.h")).read()
+    assert "#define T0MI_NOALLOC_SCRATCH_BYTES (32u << 20)" in text and t0mi.NOALLOC_SCRATCH_BYTES == 32 << 20
+    sk4 = cfg.copy(split_k=4)
+    rt.gemm_noalloc(sk4, 0x1000, 0x2000, 0x3000, 512, 4096, 256)  # 4 planes of 8 MiB: fits exactly
+    for m, n, k, c in ((513, 4096, 256, sk4), (4096, 4096, 0, cfg)):  # one row more; K = 0 zero plane of 64 MiB
+        with pytest.raises(t0mi.T0miError) as e:
+            rt.gemm_noalloc(c, 0x1000, 0x2000, 0x3000, m, n, k)
+        assert e.value.code == t0mi.ERR_INVALID and "scratch" in str(e.value)
+    with pytest.raises(t0mi.T0miError):
+        rt.gemm_noalloc(cfg, 0x1000, 0x2000, 0x3000, 64, 64, 100)  # K % 8, as t0mi_gemm
     # W4A16 alignment contract: A, qweight and Y 16-byte, scales 8-byte, qzeros 4-byte
     # (checked before the null backend returns).
     w4 = t0mi.Runtime(null=True)
