@@ -37,6 +37,7 @@
 #include <utility>
 
 #include "epi_chain.h"
+#include "index_maps.h"
 
 namespace t0mi {
 
@@ -138,25 +139,7 @@ __device__ __forceinline__ void store_block(const GemmParams& p, const f32x16& a
   }
 }
 
-// XOR swizzle of 16-byte chunks inside a K-contiguous LDS row of KC chunks.
-// Any 8 consecutive rows (aligned to 8) reading the same logical chunk land in
-// 8 distinct 16-byte slots of a 128-byte bank line.
-// Only the low 5 row bits are used, so rows 32 apart share the swizzle.
-template <int KC>
-__device__ __forceinline__ int swz(int r) {
-  constexpr int RPL = 8 / KC;  // rows per 128-byte line
-  return ((r / RPL) ^ ((r >> 3) & 3)) & (KC - 1);
-}
-
-// Swizzle of the 16-byte chunks of an NN B row (row = k, NC chunks per row).
-// A transpose read is served 32 lanes at a time: two 16-lane groups that read
-// the same 4 consecutive rows, 32 bytes each, in adjacent 32-byte column slots
-// (2j, 2j+1).  XOR of the chunk index with 4*(k % 4) moves row k to slot
-// offset 2*(k % 4), so the 4 rows x 2 slots cover 8 distinct 32-byte slots:
-// all 64 banks, no conflict.  Rows of 8 chunks (tile_n = 64) have only 4
-// slots; there 2*(k % 4) keeps each 16-lane group conflict-free.
-template <int NC>
-__device__ __forceinline__ int swz_nn(int k) { return NC >= 16 ? (k & 3) << 2 : (k & 3) << 1; }
+// swz / swz_nn (the LDS swizzles) and the DMA chunk maps: index_maps.h.
 
 // Linear workgroup id -> (tile_m, tile_n, partition).
 // Workgroups are dispatched round-robin over the 8 XCDs; with xcd_remap the
@@ -343,9 +326,8 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_bf16_kernel(GemmParams p) {
   int a_kofs[NA], b_kofs[NB];  // K offset of the lane's chunk inside a tile
 #pragma unroll
   for (int j = 0; j < NA; ++j) {
-    const int q = (wave_s + j * T::NWAVES) * 64 + lane;
-    const int row = q / KC, pc = q % KC;
-    const int lc = pc ^ swz<KC>(row);
+    int row, lc;
+    kc_dma_chunk<KC>((wave_s + j * T::NWAVES) * 64 + lane, &row, &lc);
     int gr = m0 + row;
     gr = gr < (int)p.M ? gr : (int)p.M - 1;
     a_src[j] = p.a + (size_t)gr * p.lda + kbeg + lc * 8;
@@ -355,15 +337,15 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_bf16_kernel(GemmParams p) {
   for (int j = 0; j < NB; ++j) {
     const int q = (wave_s + j * T::NWAVES) * 64 + lane;
     if constexpr (!NN) {
-      const int row = q / KC, pc = q % KC;
-      const int lc = pc ^ swz<KC>(row);
+      int row, lc;
+      kc_dma_chunk<KC>(q, &row, &lc);
       int gr = n0 + row;
       gr = gr < (int)p.N ? gr : (int)p.N - 1;
       b_src[j] = p.b + (size_t)gr * p.ldb + kbeg + lc * 8;
       b_kofs[j] = lc * 8;
     } else {
-      const int row = q / NC, pc = q % NC;  // row = k within the tile
-      const int lc = pc ^ swz_nn<NC>(row);
+      int row, lc;  // row = k within the tile
+      nn_dma_chunk<NC>(q, &row, &lc);
       int gn = n0 + lc * 8;
       gn = gn < (int)p.N ? gn : (int)p.N - 8;
       b_src[j] = p.b + (size_t)(kbeg + row) * p.ldb + gn;
@@ -422,8 +404,8 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_bf16_kernel(GemmParams p) {
 #pragma unroll
   for (int ks = 0; ks < KS; ++ks) {
     const int c = ks * 2 + lhalf;
-    a_off[ks] = (wm * TM + lrow) * BK + ((c ^ swz<KC>(lrow)) * 8);
-    b_off[ks] = (wn * TN + lrow) * BK + ((c ^ swz<KC>(lrow)) * 8);
+    a_off[ks] = kc_slot<KC>(wm * TM + lrow, c) * 8;
+    b_off[ks] = kc_slot<KC>(wn * TN + lrow, c) * 8;
   }
   // NN transpose read: 16-lane group g, lane i addresses row
   // k = ks*16 + 8*(g>>1) + 4*r + (i>>2), columns col0 + 16*(g&1) + 4*(i&3) .. +3.
@@ -445,7 +427,7 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_bf16_kernel(GemmParams p) {
     } else {
       constexpr int fn = (r - FM) / 2, h = (r - FM) % 2;
       const int col = nn_col0 + fn * 32;
-      const int eoff = (((col >> 3) ^ nn_sw) << 3) + (col & 4);
+      const int eoff = nn_col_off(col, nn_sw);
       const int krow = ks * 16 + 4 * h + nn_krow0;
       trh[fn][h] = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
           (__attribute__((address_space(3))) i16x4*)(Bs + krow * BN + eoff));
@@ -470,7 +452,7 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_bf16_kernel(GemmParams p) {
 #pragma unroll
       for (int fn = 0; fn < FN; ++fn) {
         const int col = nn_col0 + fn * 32;
-        const int eoff = (((col >> 3) ^ nn_sw) << 3) + (col & 4);
+        const int eoff = nn_col_off(col, nn_sw);
         i16x4 v[2];
 #pragma unroll
         for (int r = 0; r < 2; ++r) {

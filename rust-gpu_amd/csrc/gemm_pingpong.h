@@ -130,15 +130,17 @@ __global__ __launch_bounds__(512) void gemm_bf16_pingpong_kernel(GemmParams p) {
   // uniform base.
   uint32_t a_voff, b_voff;
   {
-    const int row = w4 * 8 + (lane >> 3), pc = lane & 7;
-    a_voff = (uint32_t)(row * (int)p.lda + ((pc ^ swz<KC>(row)) * 8)) * 2u;
+    int row, lc;  // block w4 of the group's half tile: rows 8 w4 .. 8 w4 + 7
+    kc_dma_chunk<KC>(w4 * 64 + lane, &row, &lc);
+    a_voff = (uint32_t)(row * (int)p.lda + lc * 8) * 2u;
     if constexpr (NN) {
-      const int brow = 2 * (16 * g + w4) + (lane >> 5), bpc = lane & 31;
-      int gn = n0 + ((bpc ^ swz_nn<NC>(brow)) * 8);
+      int brow, blc;  // block 16g + w4: k-rows 2 (16g + w4) and the next
+      nn_dma_chunk<NC>((16 * g + w4) * 64 + lane, &brow, &blc);
+      int gn = n0 + blc * 8;
       gn = gn < (int)p.N ? gn : (int)p.N - 8;
       b_voff = (uint32_t)(brow * (int)p.ldb + gn) * 2u;
     } else {
-      b_voff = (uint32_t)(row * (int)p.ldb + ((pc ^ swz<KC>(row)) * 8)) * 2u;
+      b_voff = (uint32_t)(row * (int)p.ldb + lc * 8) * 2u;
     }
   }
   // A through four buffer resources, one per 32-row block j of this group's
@@ -191,8 +193,8 @@ __global__ __launch_bounds__(512) void gemm_bf16_pingpong_kernel(GemmParams p) {
   int a_off[KS], b_off[NN ? 1 : KS];
 #pragma unroll
   for (int ks = 0; ks < KS; ++ks) {
-    a_off[ks] = lrow * BK + (((ks * 2 + lhalf) ^ swz<KC>(lrow)) * 8);
-    if constexpr (!NN) b_off[ks] = (wn * TN + lrow) * BK + (((ks * 2 + lhalf) ^ swz<KC>(lrow)) * 8);
+    a_off[ks] = kc_slot<KC>(lrow, ks * 2 + lhalf) * 8;
+    if constexpr (!NN) b_off[ks] = kc_slot<KC>(wn * TN + lrow, ks * 2 + lhalf) * 8;
   }
   const int tg = lane >> 4, ti = lane & 15;
   const int nn_krow0 = 8 * (tg >> 1) + (ti >> 2);
@@ -211,7 +213,7 @@ __global__ __launch_bounds__(512) void gemm_bf16_pingpong_kernel(GemmParams p) {
     } else {
       constexpr int fn = (r - FM) / 2, h = (r - FM) % 2;
       const int col = nn_col0 + fn * 32;
-      const int eoff = (((col >> 3) ^ nn_sw) << 3) + (col & 4);
+      const int eoff = nn_col_off(col, nn_sw);
       const int krow = ks * 16 + 4 * h + nn_krow0;
       tr[ks][fn][h] = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
           (__attribute__((address_space(3))) i16x4*)(Bs + krow * BN + eoff));

@@ -99,7 +99,6 @@ template <int NW, int KBW, int KBPG, bool ZEROS, int CH = 1, int RS = 1>
 __global__ __launch_bounds__(NW * 64) void w4a16_decode_v2(W4Params p) {
   static_assert(KBW % KBPG == 0, "whole groups per wave");
   static_assert(RS >= 1 && RS <= 4, "one to four row slabs");
-  constexpr int NG = KBW / KBPG;
   // CH chunks per wave: chunk c's loads are issued, then its blocks computed,
   // before chunk c+1's loads (CB blocks, whole groups and pairs per chunk).
   constexpr int CB = KBW / CH;
@@ -128,7 +127,7 @@ __global__ __launch_bounds__(NW * 64) void w4a16_decode_v2(W4Params p) {
   // values) per instruction, stored to LDS and read back in the MFMA layout
   // with ds_read_b128.  Piece (row 8h + r, 16-byte chunk x) of the block
   // (pair p, half h) sits in slot
-  //   slot(h, r, x) = 16 * (x >> 1) + ((8h + r) ^ (8 * (x & 1) + (x >> 1))),
+  //   dec_slot(h, r, x) = 16 * (x >> 1) + ((8h + r) ^ (8 * (x & 1) + (x >> 1))),
   // so for a fixed chunk the 16 rows fall in 16 distinct 16-byte bank groups
   // and the fragment reads (16 rows x one chunk per 16 lanes) are free of bank
   // conflicts.
@@ -148,13 +147,12 @@ __global__ __launch_bounds__(NW * 64) void w4a16_decode_v2(W4Params p) {
   // the 8-row half; the two rows' slot sets are disjoint, so the stores are
   // conflict-free too.
   const int ld_r = (lane >> 4) + 4 * ((lane >> 3) & 1), ld_x = lane & 7;
-  auto slot = [](int h, int r, int x) { return 16 * (x >> 1) + ((8 * h + r) ^ (8 * (x & 1) + (x >> 1))); };
-  const int st_off[2] = {16 * slot(0, ld_r, ld_x), 1024 + 16 * slot(1, ld_r, ld_x)};
+  const int st_off[2] = {16 * dec_slot(0, ld_r, ld_x), 1024 + 16 * dec_slot(1, ld_r, ld_x)};
   int rd_off[2];  // fragment byte offset for k-block parity 0 / 1
 #pragma unroll
   for (int beta = 0; beta < 2; ++beta) {
     const int h = c >> 3, r = c & 7, x = 4 * beta + g;
-    rd_off[beta] = h * 1024 + 16 * slot(h, r, x);
+    rd_off[beta] = h * 1024 + 16 * dec_slot(h, r, x);
   }
 
   // FULL: all KBW blocks of the wave exist (every wave but those at the ragged

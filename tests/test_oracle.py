@@ -242,6 +242,57 @@ def test_w4a16_oracle_is_dequant_then_gemm():
     assert np.array_equal(y, ref)
 
 
+@pytest.mark.parametrize("zeros", [False, True])
+def test_w4a16_oracle_against_float64_brute_force_from_raw_nibbles(zeros):
+    """orc_w4a16_gemm pinned by a float64 brute force written from the definitions
+    alone, in pure Python: the packed words are assembled bit by bit from raw
+    nibbles (word (kk, n) holds q[8kk+e][n] in bits 4e..4e+3, quant_kernels.rs:3-10),
+    zero points either the constant 8 or a nibble per (group, column) (u32 word
+    (g, n/8), bits 4(n%8)), w = (q - z) * s (quant_kernels.rs:24, 95-100).
+    The oracle sums in fp32, so it may differ from the float64 sum by at most
+    K * 2^-24 * sum|a w| per output; a swapped nibble order, a transposed word, a
+    wrong group index or a dropped zero point is off by far more."""
+    import random
+    import struct
+    M, K, N, g = 2, 256, 32, 128
+    rnd = random.Random(1234 + zeros)
+    q = [[rnd.randrange(16) for _ in range(N)] for _ in range(K)]
+    z = [[rnd.randrange(16) if zeros else 8 for _ in range(N)] for _ in range(K // g)]
+    # bf16 bit patterns: activations roughly N(0,1), scales in [2^-8, 2^-5)
+    def bf16_bits(x):
+        return struct.unpack("<I", struct.pack("<f", x))[0] >> 16
+    def bits_to_float(h):
+        return struct.unpack("<f", struct.pack("<I", h << 16))[0]
+    a_bits = [[bf16_bits(rnd.gauss(0.0, 1.0)) for _ in range(K)] for _ in range(M)]
+    s_bits = [[bf16_bits(2.0 ** rnd.uniform(-8, -5)) for _ in range(N)] for _ in range(K // g)]
+    words = [[sum(q[8 * kk + e][n] << (4 * e) for e in range(8)) for n in range(N)] for kk in range(K // 8)]
+    zwords = [[sum(z[gi][8 * nn + e] << (4 * e) for e in range(8)) for nn in range(N // 8)]
+              for gi in range(K // g)]
+    y64 = [[0.0] * N for _ in range(M)]
+    bound = [[0.0] * N for _ in range(M)]
+    for i in range(M):
+        for n in range(N):
+            acc = mag = 0.0
+            for k in range(K):
+                wv = (q[k][n] - z[k // g][n]) * bits_to_float(s_bits[k // g][n])
+                av = bits_to_float(a_bits[i][k])
+                acc += av * wv
+                mag += abs(av * wv)
+            y64[i][n], bound[i][n] = acc, mag
+    a = np.array(a_bits, np.uint16)
+    w = np.array(words, np.uint32)
+    s = np.array(s_bits, np.uint16)
+    zw = np.array(zwords, np.uint32) if zeros else None
+    y = oracle.w4a16_gemm(a, w, s, zw, g, 8)
+    y64, bound = np.array(y64), np.array(bound)
+    err = np.abs(y.astype(np.float64) - y64)
+    assert np.all(err <= K * 2.0 ** -24 * bound + 1e-30), float((err / (bound + 1e-30)).max())
+    # the check has teeth: the same sums with the nibbles read high-first miss it
+    q_swapped = oracle.unpack_qweight(w)[np.arange(K) ^ 7]
+    y_bad = oracle.w4a16_gemm(a, oracle.pack_qweight(q_swapped), s, zw, g, 8)
+    assert np.any(np.abs(y_bad.astype(np.float64) - y64) > K * 2.0 ** -24 * bound)
+
+
 # ------------------------------------------------------- epilogue chain ----
 
 def test_epilogue_closed_forms():
