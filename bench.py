@@ -34,12 +34,25 @@ def parse():
     p.add_argument("--gpus", type=int, default=1)
     p.add_argument("--steps", type=int, default=200)
     p.add_argument("--warmup", type=int, default=10)
-    p.add_argument("--only", choices=["all", "gemm", "w4a16", "skinny", "prefill", "copy", "dispatch"],
+    p.add_argument("--only", choices=["all", "gemm", "w4a16", "skinny", "prefill", "copy", "dispatch", "stream",
+                                      "mfma"],
                    default="all",
                    help="'copy' runs only a plain 1 GiB fp32 copy kernel: the calibration for rocprofv3 "
                         "FETCH_SIZE/WRITE_SIZE readings; 'dispatch' times batched submission (a batch of "
                         "small GEMM dispatches: synchronous, DispatchQueue, HIP graph); 'skinny' and "
-                        "'prefill' time BASELINE configs 3 and 5 (parity shapes, not the headline line)")
+                        "'prefill' time BASELINE configs 3 and 5 (parity shapes, not the headline line); "
+                        "'stream' times the probe floors of the W4A16 decode (a streaming read of its bytes "
+                        "over rotated copies, and an empty launch); 'mfma' a pure MFMA loop on random and "
+                        "zero operands with its shader clock")
+    p.add_argument("--stream-bytes", type=int, default=0,
+                   help="with --only stream: bytes per launch (default: the decode's 23,732,224); with "
+                        "--stream-calibrate one non-temporal pass over this many bytes")
+    p.add_argument("--stream-calibrate", action="store_true",
+                   help="with --only stream: run only non-temporal 16-byte read passes of --stream-bytes "
+                        "(default 1 GiB), the FETCH_SIZE calibration for the decode's load type")
+    p.add_argument("--clocks", action="store_true",
+                   help="with --only gemm / w4a16 / mfma: sample the GPU clock and power (amd-smi) during ~3 s of "
+                        "sustained launches and report their medians")
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     p.add_argument("--config", default=None, help="GEMM preset name to force (default: auto_select)")
     p.add_argument("--rows", type=int, default=16,
@@ -99,6 +112,7 @@ def bench_gemm(args, torch, t0mi, rt):
     print(f"[bench] gemm {cfg.name()} 4096^3 NN bf16-out: {us:.1f} us/launch (median of {len(batches)} batches "
           f"of {args.steps}: {', '.join(f'{b:.1f}' for b in batches)}), {tflops:.1f} TFLOPS "
           f"({100*tflops/PEAK_BF16_TFLOPS:.1f}% of peak); host wall {t_host:.3f}s", file=sys.stderr, flush=True)
+    args.gemm_clocks = smi_sample(3.0, lambda: rt.gemm(cfg, pa, pb, py, M, N, K), torch) if args.clocks else None
     return cfg, ms, tflops, batches
 
 
@@ -225,12 +239,49 @@ def bench_w4a16(args, torch, t0mi, rt):
         pw, ps = wp[i % copies]
         rt.w4a16_gemm(pa, pw, ps, 0, 8, py, Mw, Kw, Nw, G, t0mi.OUT_BF16)
     us, batches = timed_batches(torch, launch_i, calls)
+    args.w4_graph_us = w4a16_graph_us(torch, t0mi, pa, wp, py, Mw, Kw, Nw, G, copies)
+    args.w4_clocks = smi_sample(3.0, launch, torch) if args.clocks else None
     alg_bytes = 2 * Mw * Kw + Kw * Nw // 2 + 2 * (Kw // G) * Nw + 2 * Mw * Nw
     gbs = alg_bytes / (us * 1e-6) / 1e9
     print(f"[bench] w4a16 decode {Mw}x4096x11008 g128: {us:.2f} us/call (median of {len(batches)} batches of "
           f"{calls}: {', '.join(f'{b:.2f}' for b in batches)}), {gbs:.0f} GB/s "
           f"({100*gbs/PEAK_HBM_GBS:.1f}% of HBM peak), {copies} weight copies rotated", file=sys.stderr, flush=True)
     return us, gbs, alg_bytes, copies, batches
+
+
+def w4a16_graph_us(torch, t0mi, pa, wp, py, Mw, Kw, Nw, G, copies):
+    """Per-call time of the same decode calls replayed from a HIP graph (captured with the
+    runtime's capture API on its own stream): the kernels back to back without the host's
+    enqueue cost (~4 us per call from Python), which bounds what direct launches can show
+    once a call's kernel time falls below it.  Median of the replays' per-call times."""
+    rt2 = t0mi.Runtime(device=0)
+    try:
+        ext = torch.cuda.ExternalStream(rt2.stream)
+        torch.cuda.synchronize()
+        for pw, ps in wp:  # grow the runtime's buffers before capturing
+            rt2.w4a16_gemm(pa, pw, ps, 0, 8, py, Mw, Kw, Nw, G, t0mi.OUT_BF16)
+        t0mi.check(rt2.wait_idle())
+        n = 4 * copies
+        rt2.capture_begin()
+        for i in range(n):
+            pw, ps = wp[i % copies]
+            rt2.w4a16_gemm(pa, pw, ps, 0, 8, py, Mw, Kw, Nw, G, t0mi.OUT_BF16)
+        graph = rt2.capture_end()
+        vals = []
+        for rep in range(3 + BATCHES):
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record(ext)
+            graph.launch()
+            e1.record(ext)
+            t0mi.check(rt2.wait_idle())
+            e1.synchronize()
+            if rep >= 3:
+                vals.append(e0.elapsed_time(e1) * 1e3 / n)
+        graph.destroy()
+        vals.sort()
+        return round(vals[len(vals) // 2], 3)
+    finally:
+        rt2.close()
 
 
 def cpu_model() -> str:
@@ -311,6 +362,157 @@ def copy_calibration(args, torch):
     nbytes = 2 * 4 * n
     print(json.dumps({"calibration": "fp32 copy y = x + 1", "read_bytes": 4 * n, "write_bytes": 4 * n,
                       "ms_per_launch": round(ms, 4), "GB/s": round(nbytes / (ms * 1e-3) / 1e9, 1)}), flush=True)
+
+
+def smi_sample(duration_s, launch, torch):
+    """GFX clocks (MHz, averaged over the XCDs) and socket power (W) read with amd-smi
+    every ~0.3 s while `launch` runs back to back for duration_s; medians and samples."""
+    import re
+    import subprocess
+    import threading
+    samples, stop = [], threading.Event()
+
+    def poll():
+        while not stop.is_set():
+            try:
+                out = subprocess.run(["amd-smi", "metric", "-g", "0", "-c", "-p"], capture_output=True, text=True,
+                                     timeout=10).stdout
+            except (OSError, subprocess.SubprocessError):
+                return
+            clks = [int(v) for v in re.findall(r"GFX_\d+:\s*\n\s*CLK:\s*(\d+)\s*MHz", out)]
+            pw = re.findall(r"(?:SOCKET_POWER|POWER)\s*:\s*([\d.]+)\s*W", out)
+            if clks:
+                samples.append((sum(clks) / len(clks), float(pw[0]) if pw else None))
+            stop.wait(0.3)
+    th = threading.Thread(target=poll, daemon=True)
+    t0 = time.perf_counter()
+    th.start()
+    while time.perf_counter() - t0 < duration_s:
+        for _ in range(10):
+            launch()
+        torch.cuda.synchronize()
+    stop.set()
+    th.join(timeout=15)
+    # the first sample may predate the load's steady state
+    use = samples[1:] if len(samples) > 2 else samples
+    med = lambda v: sorted(v)[len(v) // 2] if v else None
+    return {"gfx_clock_MHz_median": med([c for c, _ in use]),
+            "power_W_median": med([p for _, p in use if p is not None]),
+            "samples": len(use), "clock_MHz_samples": [round(c) for c, _ in use]}
+
+
+def bench_stream(args, torch):
+    """Probe floors of the W4A16 decode: one streaming read of its algorithmic bytes per
+    launch (16-byte loads, non-temporal and normal; rotated over >= 512 MB of copies, as
+    the decode's weights are), at several grid sizes, and an empty launch."""
+    from t0mi import probes
+    stream_ptr = torch.cuda.current_stream().cuda_stream
+    sink = torch.zeros(1 << 16, device="cuda:0", dtype=torch.int32)
+    if args.stream_calibrate:
+        nbytes = args.stream_bytes or (1 << 30)
+        buf = torch.zeros(nbytes, device="cuda:0", dtype=torch.uint8)
+        for _ in range(max(1, args.steps)):
+            probes.stream(stream_ptr, buf.data_ptr(), nbytes, True, 2048, sink.data_ptr())
+        torch.cuda.synchronize()
+        print(json.dumps({"calibration": "non-temporal 16-byte streaming read", "read_bytes": nbytes,
+                          "launches": max(1, args.steps)}), flush=True)
+        return
+    nbytes = args.stream_bytes or 23732224
+    nbytes -= nbytes % 16
+    copies = max(2, -(-512 * 1024 * 1024 // nbytes))
+    buf = torch.zeros(copies * nbytes, device="cuda:0", dtype=torch.uint8)
+    base = buf.data_ptr()
+    calls = max(args.steps * 4, 2 * copies)
+    res = {}
+    for nt in (True, False):
+        for grid in (256, 512, 1024, 2048):
+            launch = lambda i, nt=nt, grid=grid: probes.stream(stream_ptr, base + (i % copies) * nbytes, nbytes, nt,
+                                                              grid, sink.data_ptr())
+            warm_up(torch, lambda: launch(0), args.warmup)
+            us, batches = timed_batches(torch, launch, calls)
+            res[f"{'nt' if nt else 'normal'}_grid{grid}"] = {"us": round(us, 3),
+                                                              "GB/s": round(nbytes / (us * 1e-6) / 1e9, 1),
+                                                              "batch_us": [round(b, 3) for b in batches]}
+    empty = {}
+    for grid in (172, 256, 1024):
+        launch = lambda i, grid=grid: probes.empty(stream_ptr, grid, sink.data_ptr())
+        warm_up(torch, lambda: launch(0), args.warmup)
+        us, batches = timed_batches(torch, launch, calls)
+        empty[f"grid{grid}"] = {"us": round(us, 3), "batch_us": [round(b, 3) for b in batches]}
+    best = min(res.items(), key=lambda kv: kv[1]["us"])
+    # The same launches replayed from a HIP graph: no host enqueue cost between them (a
+    # Python-driven launch costs ~3 us of host time, more than an empty kernel's GPU time).
+    best_nt = best[0].startswith("nt")
+    best_grid = int(best[0].split("grid")[1])
+    side = torch.cuda.Stream()
+    graphs = {}
+    with torch.cuda.stream(side):
+        for name, fn, n in (("stream_" + best[0], lambda k: probes.stream(side.cuda_stream, base + (k % copies) * nbytes,
+                                                                          nbytes, best_nt, best_grid, sink.data_ptr()),
+                             4 * copies),
+                            ("empty_grid256", lambda k: probes.empty(side.cuda_stream, 256, sink.data_ptr()), 200)):
+            gr = torch.cuda.CUDAGraph()
+            torch.cuda.synchronize()
+            with torch.cuda.graph(gr, stream=side):
+                for k in range(n):
+                    fn(k)
+            torch.cuda.synchronize()
+            vals = []
+            for rep in range(3 + BATCHES):
+                e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                e0.record(side)
+                gr.replay()
+                e1.record(side)
+                torch.cuda.synchronize()
+                if rep >= 3:
+                    vals.append(e0.elapsed_time(e1) * 1e3 / n)
+            vals.sort()
+            graphs[name] = {"us": round(vals[len(vals) // 2], 3), "launches_per_replay": n,
+                            "replay_us_per_launch": [round(v, 3) for v in vals]}
+    g_us = graphs["stream_" + best[0]]["us"]
+    print(json.dumps({"metric": "streaming-read floor of the W4A16 decode's bytes", "unit": "us/launch",
+                      "higher_is_better": False, "bytes_per_launch": nbytes, "copies_rotated": copies,
+                      "launches_per_batch": calls, "timing": f"median of {BATCHES} batches (HIP events)",
+                      "best": {"case": best[0], **best[1]},
+                      "graph_replay": graphs,
+                      "floor_GB/s_graph": round(nbytes / (g_us * 1e-6) / 1e9, 1),
+                      "floor_frac_graph": round(nbytes / (g_us * 1e-6) / 1e9 / PEAK_HBM_GBS, 4),
+                      "stream": res, "empty_kernel_256_threads": empty}),
+          flush=True)
+
+
+def bench_mfma(args, torch):
+    """Pure MFMA loop (probe_mfma: the ping-pong kernel's per-tile MFMA pattern, 8 waves per
+    CU, 256 workgroups) on random N(0,1) and on zero bf16 operands: TFLOP/s and the shader
+    clock from s_memtime / s_memrealtime (100 MHz) stamps; with --clocks also amd-smi."""
+    from t0mi import probes
+    stream_ptr = torch.cuda.current_stream().cuda_stream
+    n_frag, grid, iters = 1 << 16, 256, 4000
+    g = torch.Generator(device="cuda:0")
+    g.manual_seed(0x7701)
+    srcs = {"random": torch.randn(n_frag * 8, device="cuda:0", generator=g).to(torch.bfloat16),
+            "zero": torch.zeros(n_frag * 8, device="cuda:0", dtype=torch.bfloat16)}
+    out = torch.empty(grid * 512, device="cuda:0", dtype=torch.float32)
+    stamps = torch.zeros(grid * 4, device="cuda:0", dtype=torch.int64)
+    flop = grid * 8 * iters * probes.MFMA_FLOP_PER_ITER_WAVE
+    res = {}
+    for name, src in srcs.items():
+        launch = lambda i=0, src=src: probes.mfma(stream_ptr, src.data_ptr(), n_frag, iters, grid, out.data_ptr(),
+                                                  stamps.data_ptr())
+        warm_up(torch, lambda: launch(), 2, min_s=1.0)
+        us, batches = timed_batches(torch, launch, 20)
+        st = stamps.view(grid, 4).cpu().numpy().astype("float64")
+        clk = (st[:, 1] - st[:, 0]) / (st[:, 3] - st[:, 2]) * 100.0  # MHz: shader cycles per 10 ns tick
+        clk.sort()
+        res[name] = {"us_per_launch": round(us, 1), "TFLOP/s": round(flop / (us * 1e-6) / 1e12, 1),
+                     "frac_of_peak": round(flop / (us * 1e-6) / 1e12 / PEAK_BF16_TFLOPS, 4),
+                     "shader_clock_MHz_median": round(float(clk[len(clk) // 2]), 1),
+                     "batch_us": [round(b, 1) for b in batches]}
+        if args.clocks:
+            res[name]["amd_smi"] = smi_sample(3.0, launch, torch)
+    print(json.dumps({"metric": "pure MFMA loop v_mfma_f32_32x32x16_bf16", "unit": "TFLOP/s",
+                      "workload": f"{grid} workgroups x 8 waves x {iters} iterations of 32 MFMAs",
+                      "peak": PEAK_BF16_TFLOPS, "results": res}), flush=True)
 
 
 def bench_dispatch(args, torch, t0mi):
@@ -397,6 +599,12 @@ def main():
     if args.only == "copy":
         copy_calibration(args, torch)
         return
+    if args.only == "stream":
+        bench_stream(args, torch)
+        return
+    if args.only == "mfma":
+        bench_mfma(args, torch)
+        return
     import t0mi
     if args.only == "dispatch":
         bench_dispatch(args, torch, t0mi)
@@ -440,6 +648,8 @@ def main():
                                "M": 4096, "N": 4096, "K": 4096, "kernel": cfg.name()}})
         if args.tuned:
             out["tuned"] = args.tuned
+        if args.gemm_clocks:
+            out["clocks_during_sustained_launches"] = args.gemm_clocks
         traffic = load_traffic("gemm_4096")
         out["roofline"] = {"bound": "mfma", "achieved": round(tflops, 2), "peak": PEAK_BF16_TFLOPS,
                            "unit": "TFLOP/s", "frac": round(tflops / PEAK_BF16_TFLOPS, 4), "traffic": traffic}
@@ -448,6 +658,8 @@ def main():
         w = {"value": round(gbs, 1), "unit": "GB/s", "us_per_call": round(us, 3),
              "batch_us": [round(b, 3) for b in wb],
              "frac_of_peak": round(gbs / PEAK_HBM_GBS, 4), "algorithmic_bytes": alg_bytes,
+             "graph_replay_us_per_call": args.w4_graph_us,
+             **({"clocks_during_sustained_launches": args.w4_clocks} if args.w4_clocks else {}),
              "weight_copies_rotated": copies,
              "workload": f"W4A16 decode A[{args.rows},4096] bf16 x int4 W[4096,11008] g128 zp=8, bf16 out"
                          + (" (BASELINE config 4)" if args.rows == 16 else "")}

@@ -1,0 +1,46 @@
+"""ctypes binding of libt0mi_probes.so: the measurement kernels behind the floors the
+GEMM and W4A16 kernels are judged against (streaming read with 16-byte normal or
+non-temporal loads, empty launch, pure MFMA loop with shader-clock stamps).  Used by
+bench.py --only stream / mfma; not part of the product ABI."""
+import ctypes
+import os
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+PROBES_PATH = os.path.join(_HERE, "libt0mi_probes.so")
+_lib = None
+
+
+def lib():
+    global _lib
+    if _lib is None:
+        if not os.path.exists(PROBES_PATH):
+            raise ImportError(f"libt0mi_probes.so not built at {PROBES_PATH}; run __graft_entry__.build()")
+        L = ctypes.CDLL(PROBES_PATH)
+        P, U32, SZ, I = ctypes.c_void_p, ctypes.c_uint32, ctypes.c_size_t, ctypes.c_int
+        L.t0mi_probe_stream.argtypes = [P, P, SZ, I, U32, P]
+        L.t0mi_probe_empty.argtypes = [P, U32, P]
+        L.t0mi_probe_mfma.argtypes = [P, P, U32, U32, U32, P, P]
+        for f in (L.t0mi_probe_stream, L.t0mi_probe_empty, L.t0mi_probe_mfma):
+            f.restype = I
+        _lib = L
+    return _lib
+
+
+def _check(rc, what):
+    if rc != 0:
+        raise RuntimeError(f"{what} failed ({rc})")
+
+
+def stream(stream_ptr, src, nbytes, nt, grid, sink):
+    _check(lib().t0mi_probe_stream(stream_ptr, src, nbytes, 1 if nt else 0, grid, sink), "t0mi_probe_stream")
+
+
+def empty(stream_ptr, grid, sink):
+    _check(lib().t0mi_probe_empty(stream_ptr, grid, sink), "t0mi_probe_empty")
+
+
+def mfma(stream_ptr, src, n_frag, iters, grid, out, stamps):
+    _check(lib().t0mi_probe_mfma(stream_ptr, src, n_frag, iters, grid, out, stamps), "t0mi_probe_mfma")
+
+
+MFMA_FLOP_PER_ITER_WAVE = 2 * 32 * 32 * 16 * 32  # 32 MFMAs 32x32x16 per iteration and wave

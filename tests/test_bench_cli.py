@@ -48,3 +48,19 @@ def test_leg_prints_one_json_line(leg, unit, bound):
     assert roof["bound"] == bound and 0 < roof["frac"] < 1
     assert roof["frac"] == pytest.approx(roof["achieved"] / roof["peak"], rel=1e-3)
     assert roof["traffic"] > 0
+
+
+@pytest.mark.gpu
+def test_probe_floors_print_one_json_line():
+    """--only stream / mfma (libt0mi_probes.so): the decode's streaming-read and empty-launch
+    floors, and the pure-MFMA rate with its shader clock."""
+    r = run_bench("--only", "stream", "--steps", "12", "--warmup", "2")
+    assert r.returncode == 0, r.stderr[-2000:]
+    out = json.loads(r.stdout.strip().splitlines()[-1])
+    assert out["bytes_per_launch"] == 23732224 and out["copies_rotated"] * out["bytes_per_launch"] >= 512 << 20
+    assert 0 < out["best"]["us"] < 1000 and all(v["us"] > 0 for v in out["empty_kernel_256_threads"].values())
+    r = run_bench("--only", "mfma", "--steps", "2", "--warmup", "1")
+    assert r.returncode == 0, r.stderr[-2000:]
+    res = json.loads(r.stdout.strip().splitlines()[-1])["results"]
+    for name in ("random", "zero"):
+        assert 0 < res[name]["frac_of_peak"] < 1.05 and 100 < res[name]["shader_clock_MHz_median"] < 3000
