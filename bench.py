@@ -55,6 +55,8 @@ def parse():
                         "sustained launches and report their medians")
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     p.add_argument("--config", default=None, help="GEMM preset name to force (default: auto_select)")
+    p.add_argument("--split-k", type=int, default=0, help="with --config: the split-K factor to force")
+    p.add_argument("--stages", type=int, default=0, help="with --config: the LDS stage count to force")
     p.add_argument("--rows", type=int, default=16,
                    help="with --only w4a16: activation rows of the decode GEMM (default 16, BASELINE config 4)")
     p.add_argument("--tune", action="store_true",
@@ -165,6 +167,10 @@ def bench_skinny(args, torch, t0mi, rt):
     y = torch.empty(M, N, device="cuda:0", dtype=torch.bfloat16)
     cfg = t0mi.preset(args.config) if args.config else t0mi.auto_select_layout(M, K, N, t0mi.NN, t0mi.OUT_BF16)
     cfg = cfg.copy(transpose=t0mi.NN, out_dtype=t0mi.OUT_BF16)
+    if args.config and args.split_k:
+        cfg = cfg.copy(split_k=args.split_k)
+    if args.config and args.stages:
+        cfg = cfg.copy(stages=args.stages)
     tuned = run_tuner(t0mi, rt, M, N, K, t0mi.NN, t0mi.OUT_BF16) if args.tune else None
     pa, py = a.data_ptr(), y.data_ptr()
 

@@ -358,8 +358,10 @@ int t0mi_tile_compute_grid(const t0mi_tile_spec* s, uint32_t m, uint32_t n, uint
  * three 16-K steps; NN tiles narrower than 64 columns on the 64-column NN
  * kernel).  The handle dispatches with the spec's own kernarg layout and grid;
  * M comes from the kernarg (0 = derive it from the grid, padded as gemm_gen
- * does), and a persistent spec's one-WG grid launches the full tile grid (same
- * results).  T0MI_ERR_NO_KERNEL when no prebuilt kernel covers the tile. */
+ * does).  A persistent spec (one workgroup looping over the N-tiles in the
+ * reference, tile_ir.rs:540-561) runs as one launch of the configuration the
+ * cost model picks for its (M, N, K), split-K included, with its epilogue.
+ * T0MI_ERR_NO_KERNEL when no prebuilt kernel covers the tile. */
 int t0mi_tile_kernel_get(t0mi_ctx* ctx, const t0mi_tile_spec* s, t0mi_kernel** out);
 /* One-call tile GEMM: Y[m,n] = epilogue(X[m,k] . B) for the spec's transpose,
  * with the chain's arguments; split_k > 1 is reduced deterministically (the

@@ -94,7 +94,7 @@ int ensure_cvt_buffer(t0mi_ctx* ctx, size_t bytes);
 // Runs a GEMM with the best prebuilt config for (m, n, k, transpose) and the
 // given output type (cost-model ranking, as t0mi_auto_select).  Asynchronous.
 int run_gemm_auto(t0mi_ctx* ctx, uint32_t transpose, uint64_t x, uint64_t b, uint64_t y, uint32_t m, uint32_t n,
-                  uint32_t k, uint32_t out_dtype = T0MI_OUT_F32);
+                  uint32_t k, uint32_t out_dtype = T0MI_OUT_F32, uint64_t bias = 0, const EpiChain* epi = nullptr);
 // Launches the bf16 GEMM kernel for (cfg, params) on ctx's stream.
 int launch_gemm(t0mi_ctx* ctx, const t0mi_gemm_config& cfg, const GemmLaunchEntry* e, GemmParams p);
 int check_ctx(t0mi_ctx* ctx);

@@ -40,6 +40,34 @@ __global__ __launch_bounds__(256) void probe_stream(const u32x4* __restrict__ sr
   if (f == never) sink[blockIdx.x] = f;
 }
 
+// 2-D block read: the matrix is `rows` rows of `pitch` bytes; workgroup (cb, rb)
+// reads rows [rb * R, rb * R + R) x bytes [cb * L, cb * L + L) with 16-byte loads
+// (non-temporal), lanes walking the block row-major, UNROLL loads in flight per
+// thread.  The access shape of a GEMM or decode workgroup's operand block.
+__global__ __launch_bounds__(256) void probe_block(const char* __restrict__ src, uint32_t pitch, uint32_t L,
+                                                  uint32_t R, uint32_t cblocks, uint32_t never,
+                                                  uint32_t* __restrict__ sink) {
+  const uint32_t cb = blockIdx.x % cblocks, rb = blockIdx.x / cblocks;
+  const uint32_t chunks = L / 16, total = chunks * R;
+  const char* base = src + (size_t)rb * R * pitch + (size_t)cb * L;
+  u32x4 acc = {0u, 0u, 0u, 0u};
+  uint32_t i = threadIdx.x;
+  for (; i + 7 * 256 < total; i += 8 * 256) {
+    u32x4 v[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      const uint32_t q = i + u * 256;
+      v[u] = __builtin_nontemporal_load((const u32x4*)(base + (size_t)(q / chunks) * pitch + (q % chunks) * 16));
+    }
+#pragma unroll
+    for (int u = 0; u < 8; ++u) acc ^= v[u];
+  }
+  for (; i < total; i += 256)
+    acc ^= __builtin_nontemporal_load((const u32x4*)(base + (size_t)(i / chunks) * pitch + (i % chunks) * 16));
+  const uint32_t f = acc.x ^ acc.y ^ acc.z ^ acc.w;
+  if (f == never) sink[blockIdx.x] = f;
+}
+
 __global__ __launch_bounds__(256) void probe_empty(uint32_t never, uint32_t* sink) {
   if (threadIdx.x == never) sink[0] = never;
 }
@@ -111,6 +139,20 @@ int t0mi_probe_stream(void* stream, const void* src, size_t bytes, int nt, uint3
   else
     hipLaunchKernelGGL((probe_stream<false, 8>), dim3(grid), dim3(256), 0, (hipStream_t)stream, (const u32x4*)src,
                        n16, 0xFFFFFFFFu, sink);
+  return launched();
+}
+
+// Reads a matrix of `rows` x `pitch` bytes once, as blocks of R rows x L bytes
+// (one workgroup of 256 threads per block; L a multiple of 16 dividing pitch,
+// R dividing rows).  sink: one u32 per workgroup (never written).
+int t0mi_probe_block(void* stream, const void* src, uint32_t rows, uint32_t pitch, uint32_t L, uint32_t R,
+                     uint32_t* sink) {
+  if (!src || !sink || L == 0 || R == 0 || (L & 15) || pitch % L || rows % R || ((uintptr_t)src & 15) ||
+      (pitch & 15))
+    return -1;
+  const uint32_t cblocks = pitch / L, grid = cblocks * (rows / R);
+  hipLaunchKernelGGL(probe_block, dim3(grid), dim3(256), 0, (hipStream_t)stream, (const char*)src, pitch, L, R,
+                     cblocks, 0xFFFFFFFFu, sink);
   return launched();
 }
 

@@ -165,6 +165,10 @@ int launch_gemm(t0mi_ctx* ctx, const t0mi_gemm_config& cfg, const GemmLaunchEntr
 // ------------------------------------------------------------ split-K reduce --
 // Deterministic reduction of split-K partial planes: y = sum_{p=0..sk-1} ws[p]
 // in ascending p, then the epilogue chain, then f32 or bf16 (RNE) store.
+// Each thread owns one 4-column vector and issues the loads of up to 16
+// planes before the first add, so a call's partials stream in one round trip
+// (the planes were just written and are mostly served by the Infinity Cache).
+template <int SK>  // planes handled with all loads in flight (0: any count, 4 at a time)
 __global__ __launch_bounds__(256) void t0mi_splitk_reduce(const float* __restrict__ ws, void* __restrict__ y,
                                                           const float* __restrict__ bias, uint32_t M, uint32_t N,
                                                           uint32_t ldy, uint32_t sk, uint32_t out_bf16,
@@ -175,26 +179,41 @@ __global__ __launch_bounds__(256) void t0mi_splitk_reduce(const float* __restric
   for (size_t v = blockIdx.x * (size_t)blockDim.x + threadIdx.x; v < nvec; v += (size_t)gridDim.x * blockDim.x) {
     const size_t idx = v * 4;
     const uint32_t m = (uint32_t)(v / nq), n = (uint32_t)(v % nq) * 4;
-    // Planes are read four at a time (independent loads in flight together)
-    // and summed in plane order, so the result does not depend on timing.
-    f32x4 s = {0.f, 0.f, 0.f, 0.f};
-    for (uint32_t q0 = 0; q0 < sk; q0 += 4) {
-      f32x4 t[4];
+    f32x4 s;
+    if constexpr (SK > 0) {
+      f32x4 t[SK];
 #pragma unroll
-      for (uint32_t j = 0; j < 4; ++j) {
-        const uint32_t q = q0 + j < sk ? q0 + j : q0;  // past the last plane: a repeat, not added
-        t[j] = *(const f32x4*)(ws + q * plane + idx);
+      for (int j = 0; j < SK; ++j) t[j] = __builtin_nontemporal_load((const f32x4*)(ws + j * plane + idx));
+      s = t[0];
+#pragma unroll
+      for (int j = 1; j < SK; ++j) {
+        s.x += t[j].x;
+        s.y += t[j].y;
+        s.z += t[j].z;
+        s.w += t[j].w;
       }
+    } else {
+      // Planes read four at a time (independent loads in flight together) and
+      // summed in plane order, so the result does not depend on timing.
+      s = f32x4{0.f, 0.f, 0.f, 0.f};
+      for (uint32_t q0 = 0; q0 < sk; q0 += 4) {
+        f32x4 t[4];
 #pragma unroll
-      for (uint32_t j = 0; j < 4; ++j) {
-        if (q0 + j >= sk) break;
-        if (q0 + j == 0) {
-          s = t[0];
-        } else {
-          s.x += t[j].x;
-          s.y += t[j].y;
-          s.z += t[j].z;
-          s.w += t[j].w;
+        for (uint32_t j = 0; j < 4; ++j) {
+          const uint32_t q = q0 + j < sk ? q0 + j : q0;  // past the last plane: a repeat, not added
+          t[j] = *(const f32x4*)(ws + q * plane + idx);
+        }
+#pragma unroll
+        for (uint32_t j = 0; j < 4; ++j) {
+          if (q0 + j >= sk) break;
+          if (q0 + j == 0) {
+            s = t[0];
+          } else {
+            s.x += t[j].x;
+            s.y += t[j].y;
+            s.z += t[j].z;
+            s.w += t[j].w;
+          }
         }
       }
     }
@@ -243,8 +262,18 @@ int launch_splitk_reduce(t0mi_ctx* ctx, const float* ws, void* y, const float* b
   const size_t nvec = (size_t)M * N / 4;
   if (nvec == 0) return T0MI_OK;
   const uint32_t blocks = (uint32_t)std::min<size_t>((nvec + 255) / 256, (size_t)ctx->cu_count * 8);
-  hipLaunchKernelGGL(t0mi_splitk_reduce, dim3(blocks), dim3(256), 0, ctx->stream, ws, y, bias, M, N, ldy, sk,
-                     out_bf16, epilogue);
+#define T0MI_REDUCE(SKC)                                                                                     \
+  hipLaunchKernelGGL(t0mi_splitk_reduce<SKC>, dim3(blocks), dim3(256), 0, ctx->stream, ws, y, bias, M, N, ldy, sk, \
+                     out_bf16, epilogue)
+  switch (sk) {
+    case 1: T0MI_REDUCE(1); break;
+    case 2: T0MI_REDUCE(2); break;
+    case 4: T0MI_REDUCE(4); break;
+    case 8: T0MI_REDUCE(8); break;
+    case 16: T0MI_REDUCE(16); break;
+    default: T0MI_REDUCE(0); break;
+  }
+#undef T0MI_REDUCE
   hipError_t e = hipGetLastError();
   return e == hipSuccess ? T0MI_OK : hip_fail(e, "reduce launch");
 }
@@ -580,6 +609,13 @@ static int dispatch_tile(t0mi_ctx* ctx, const t0mi_kernel* k, const uint32_t gri
     chain.lo = rd_f32(ka + k->lay.clamp_min);
     chain.hi = rd_f32(ka + k->lay.clamp_max);
   }
+  if (s.persistent && (sk == 1 || yss == 0))
+    // tile_ir.rs:540-561: one workgroup loops over every N-tile so that a
+    // decode-sized GEMM pays one dispatch (an RDNA scheduling workaround).  On
+    // gfx950 one workgroup is one of 256 CUs, so the spec runs as one launch of
+    // the configuration the cost model picks for (M, N, K) — split-K when the
+    // tiles alone would leave CUs idle — with the spec's epilogue.
+    return run_gemm_auto(ctx, s.transpose, x, wt, y, M, N, K, T0MI_OUT_F32, bias, &chain);
   if (sk == 1 || yss == 0)
     // One output plane: split-K partitions are summed by the library.
     return run_gemm(ctx, k->cfg, k->gemm, x, wt, y, bias, M, N, K, chain);
@@ -799,11 +835,11 @@ extern "C" int t0mi_gemm_noalloc(t0mi_ctx* ctx, const t0mi_gemm_config* cfg, uin
 }
 
 int t0mi::run_gemm_auto(t0mi_ctx* ctx, uint32_t transpose, uint64_t x, uint64_t b, uint64_t y, uint32_t m, uint32_t n,
-                        uint32_t k, uint32_t out_dtype) {
+                        uint32_t k, uint32_t out_dtype, uint64_t bias, const EpiChain* epi) {
   const std::vector<t0mi_gemm_config> cands = rank_candidates(m, n, k, transpose, out_dtype, nullptr);
   for (const t0mi_gemm_config& c : cands) {
     const GemmLaunchEntry* e = find_gemm_launch(c);
-    if (e) return run_gemm(ctx, c, e, x, b, y, 0, m, n, k, EpiChain{});
+    if (e) return run_gemm(ctx, c, e, x, b, y, bias, m, n, k, epi ? *epi : EpiChain{});
   }
   return set_error(T0MI_ERR_NO_KERNEL, "[t0mi] no prebuilt gfx950 kernel for %ux%ux%u (%s)", m, n, k,
                    transpose == T0MI_NN ? "NN" : "NT");

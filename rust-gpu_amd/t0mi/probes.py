@@ -19,8 +19,9 @@ def lib():
         P, U32, SZ, I = ctypes.c_void_p, ctypes.c_uint32, ctypes.c_size_t, ctypes.c_int
         L.t0mi_probe_stream.argtypes = [P, P, SZ, I, U32, P]
         L.t0mi_probe_empty.argtypes = [P, U32, P]
+        L.t0mi_probe_block.argtypes = [P, P, U32, U32, U32, U32, P]
         L.t0mi_probe_mfma.argtypes = [P, P, U32, U32, U32, P, P]
-        for f in (L.t0mi_probe_stream, L.t0mi_probe_empty, L.t0mi_probe_mfma):
+        for f in (L.t0mi_probe_stream, L.t0mi_probe_empty, L.t0mi_probe_mfma, L.t0mi_probe_block):
             f.restype = I
         _lib = L
     return _lib
@@ -33,6 +34,10 @@ def _check(rc, what):
 
 def stream(stream_ptr, src, nbytes, nt, grid, sink):
     _check(lib().t0mi_probe_stream(stream_ptr, src, nbytes, 1 if nt else 0, grid, sink), "t0mi_probe_stream")
+
+
+def block(stream_ptr, src, rows, pitch, run_bytes, rows_per_wg, sink):
+    _check(lib().t0mi_probe_block(stream_ptr, src, rows, pitch, run_bytes, rows_per_wg, sink), "t0mi_probe_block")
 
 
 def empty(stream_ptr, grid, sink):

@@ -149,6 +149,17 @@ def test_dispatch_persistent(rt, preset):
     assert np.array_equal(y, ref)
 
 
+@pytest.mark.parametrize("m", [1, 16])
+def test_persistent_decode_shape(rt, m):
+    """tile_persistent_decode at the decode shape it exists for (tile_ir.rs:540-561: M = 1,
+    N >= 4096): one dispatch of the cost model's configuration (split-K here), integer
+    pattern -> exact, bias + scale + clamp epilogue applied once after the reduction."""
+    spec = t0mi.tile_preset("tile_persistent_decode").copy(epilogue=[t0mi.BIAS_ADD, t0mi.SCALE, t0mi.CLAMP])
+    print(f"[tile] persistent decode m={m} n=4096 k=4096", flush=True)
+    y, ref = dispatch_case(rt, spec, m, 4096, 4096, persistent_counter=True)
+    assert np.array_equal(y, ref)
+
+
 def test_dispatch_split_k_reduced_and_planes(rt):
     m, n, k = 128, 128, 512
     spec = t0mi.tile_preset("tile_64x64_k32").copy(split_k=4, epilogue=[t0mi.NEG])
