@@ -171,21 +171,23 @@ def test_bias_relu_epilogue(rt):
             _check_tol(y2, want, a, b, k)
 
 
-def test_bench_shape_4096_sampled(rt):
-    """BASELINE config 2 at full size: 4096^3 NN, N(0,1), bf16 out.  The oracle is
-    run on 64 sampled rows; the full output is checked for row-sum consistency
-    (sum_j y[i,j] vs a[i,:] . rowsum(B)), a size-independent property."""
+def test_bench_shape_4096_full(rt):
+    """BASELINE config 2 at full size: 4096^3 NN, N(0,1), bf16 out, the bench's kernel.
+    Every one of the 16.7M outputs against the oracle (the whole GEMM on the CPU, ~1 s
+    with all cores): within one bf16 rounding of the fp32 result plus the GEMM tolerance,
+    and the relative Frobenius error bounded; the row sums (sum_j y[i,j] vs
+    a[i,:] . rowsum(B)) as a size-independent property."""
     m = n = k = 4096
     a0, b0, _, _ = oracle.seeds(1)
     a = oracle.normal_bf16((m, k), a0, 0.0, 1.0)
     b = oracle.normal_bf16((k, n), b0, 0.0, 1.0)
     cfg = t0mi.preset("gfx950_256x256_k64_w2x4").copy(transpose=t0mi.NN)
     y = oracle.bf16_to_f32(run_gemm(rt, cfg, a, b, m, n, k, out_bf16=True))
-    rows = np.linspace(0, m - 1, 64).astype(int)
-    ref = oracle.gemm_bf16(a[rows], b, "nn")
+    ref = oracle.gemm_bf16(a, b, "nn")
     tol = oracle.gemm_tolerance(k, oracle.bf16_to_f32(a), oracle.bf16_to_f32(b))
-    err, rel = oracle.compare(y[rows], ref)
+    err, rel = oracle.compare(y, ref)
     assert err <= tol and rel < 5e-3, (err, rel)
+    assert np.all(np.abs(y - ref) <= np.abs(ref) * 2.0 ** -8 + tol)
     # full-size property: row sums
     bsum = oracle.bf16_to_f32(b).astype(np.float64).sum(axis=1)
     want = oracle.bf16_to_f32(a).astype(np.float64) @ bsum

@@ -111,19 +111,21 @@ def test_w4a16_prefill_vs_oracle(rt, m, k, n, group, pgz):
     check(yb, ref_exact, a, wf, k, 6e-3)
 
 
-def test_w4a16_prefill_config5_sampled_rows(rt):
+def test_w4a16_prefill_config5_full(rt):
     """BASELINE config 5 at full size (A[4096,4096] x int4 W[4096,14336], g128, per-group
-    zeros, bf16 out); 48 rows spread over M checked against the oracle."""
+    zeros, bf16 out): all 58.7M outputs against the exact-dequant oracle (the whole GEMM
+    on the CPU, a few seconds with all cores) within the GEMM tolerance; the route rounds
+    each dequantized weight to bf16 (as the dequant kernel does), hence the 6e-3
+    relative bound."""
     m, k, n, group = 4096, 4096, 14336, 128
     a = oracle.normal_bf16((m, k), oracle.seeds(4)[0], 0.0, 1.0)
     w = oracle.pack_qweight(oracle.nibbles((k, n), oracle.seeds(4)[1]))
     s = oracle.uniform_bf16((k // group, n), oracle.seeds(4)[2], 0.005, 0.02)
     z = oracle.pack_qzeros(oracle.nibbles((k // group, n), oracle.seeds(4)[3]))
     y = run_w4a16(rt, a, w, s, z, m, k, n, group, out_bf16=True)
-    rows = np.unique(np.concatenate([np.arange(0, m, 97), [m - 1]]))[:48]
     wf = oracle.dequant_qweight_f32(w, s, z, group, 8)
-    ref = oracle.w4a16_gemm(np.ascontiguousarray(a[rows]), w, s, z, group, 8)
-    check(y[rows], ref, a[rows], wf, k, 6e-3)
+    ref = oracle.w4a16_gemm(a, w, s, z, group, 8)
+    check(y, ref, a, wf, k, 6e-3)
     assert np.isfinite(y).all()
 
 
