@@ -35,15 +35,18 @@ def parse():
     p.add_argument("--steps", type=int, default=200)
     p.add_argument("--warmup", type=int, default=10)
     p.add_argument("--only", choices=["all", "gemm", "w4a16", "skinny", "prefill", "copy", "dispatch", "stream",
-                                      "mfma"],
+                                      "mfma", "lds", "vendor"],
                    default="all",
                    help="'copy' runs only a plain 1 GiB fp32 copy kernel: the calibration for rocprofv3 "
                         "FETCH_SIZE/WRITE_SIZE readings; 'dispatch' times batched submission (a batch of "
                         "small GEMM dispatches: synchronous, DispatchQueue, HIP graph); 'skinny' and "
                         "'prefill' time BASELINE configs 3 and 5 (parity shapes, not the headline line); "
                         "'stream' times the probe floors of the W4A16 decode (a streaming read of its bytes "
-                        "over rotated copies, and an empty launch); 'mfma' a pure MFMA loop on random and "
-                        "zero operands with its shader clock")
+                        "over rotated copies, and an empty launch); 'mfma' MFMA loops of the GEMM wave tiles "
+                        "(32x32x16 / 16x16x32, operands in registers or re-read from LDS) with their shader "
+                        "clocks; 'lds' one launch per LDS read pattern (for rocprofv3 bank-conflict counters); "
+                        "'vendor' times torch.matmul (hipBLASLt) on the BASELINE GEMM shapes beside this "
+                        "library's kernels")
     p.add_argument("--stream-bytes", type=int, default=0,
                    help="with --only stream: bytes per launch (default: the decode's 23,732,224); with "
                         "--stream-calibrate one non-temporal pass over this many bytes")
@@ -488,9 +491,11 @@ def bench_stream(args, torch):
 
 
 def bench_mfma(args, torch):
-    """Pure MFMA loop (probe_mfma: the ping-pong kernel's per-tile MFMA pattern, 8 waves per
-    CU, 256 workgroups) on random N(0,1) and on zero bf16 operands: TFLOP/s and the shader
-    clock from s_memtime / s_memrealtime (100 MHz) stamps; with --clocks also amd-smi."""
+    """MFMA loops (t0mi_probes.hip probe_mfma, 256 workgroups): the ping-pong kernel's wave
+    tile (8 waves x 128x64, 32x32x16) and a 4-wave 128x128 tile with 32x32x16 or 16x16x32,
+    operands held in registers or re-read from LDS each k-step, on random N(0,1) bf16 (and
+    zeros for the ping-pong tile): TFLOP/s and the shader clock from s_memtime /
+    s_memrealtime (100 MHz) stamps; with --clocks also amd-smi clock and power."""
     from t0mi import probes
     stream_ptr = torch.cuda.current_stream().cuda_stream
     n_frag, grid, iters = 1 << 16, 256, 4000
@@ -500,25 +505,120 @@ def bench_mfma(args, torch):
             "zero": torch.zeros(n_frag * 8, device="cuda:0", dtype=torch.bfloat16)}
     out = torch.empty(grid * 512, device="cuda:0", dtype=torch.float32)
     stamps = torch.zeros(grid * 4, device="cuda:0", dtype=torch.int64)
-    flop = grid * 8 * iters * probes.MFMA_FLOP_PER_ITER_WAVE
     res = {}
-    for name, src in srcs.items():
-        launch = lambda i=0, src=src: probes.mfma(stream_ptr, src.data_ptr(), n_frag, iters, grid, out.data_ptr(),
-                                                  stamps.data_ptr())
+    runs = [(0, "zero")] + [(v, "random") for v in sorted(probes.MFMA_VARIANTS)]
+    for variant, data in runs:
+        src = srcs[data]
+        flop = grid * iters * probes.mfma_flop_per_iter(variant)
+        launch = lambda i=0, src=src, v=variant: probes.mfma(stream_ptr, src.data_ptr(), n_frag, iters, grid,
+                                                             out.data_ptr(), stamps.data_ptr(), v)
         warm_up(torch, lambda: launch(), 2, min_s=1.0)
         us, batches = timed_batches(torch, launch, 20)
         st = stamps.view(grid, 4).cpu().numpy().astype("float64")
         clk = (st[:, 1] - st[:, 0]) / (st[:, 3] - st[:, 2]) * 100.0  # MHz: shader cycles per 10 ns tick
         clk.sort()
-        res[name] = {"us_per_launch": round(us, 1), "TFLOP/s": round(flop / (us * 1e-6) / 1e12, 1),
+        name = f"v{variant}_{data}"
+        res[name] = {"variant": probes.MFMA_VARIANTS[variant][0], "operands": data,
+                     "us_per_launch": round(us, 1), "TFLOP/s": round(flop / (us * 1e-6) / 1e12, 1),
                      "frac_of_peak": round(flop / (us * 1e-6) / 1e12 / PEAK_BF16_TFLOPS, 4),
                      "shader_clock_MHz_median": round(float(clk[len(clk) // 2]), 1),
                      "batch_us": [round(b, 1) for b in batches]}
         if args.clocks:
             res[name]["amd_smi"] = smi_sample(3.0, launch, torch)
-    print(json.dumps({"metric": "pure MFMA loop v_mfma_f32_32x32x16_bf16", "unit": "TFLOP/s",
-                      "workload": f"{grid} workgroups x 8 waves x {iters} iterations of 32 MFMAs",
+        print(f"[bench] mfma {name}: {res[name]['TFLOP/s']} TFLOP/s at {res[name]['shader_clock_MHz_median']} MHz"
+              + (f", {res[name]['amd_smi']['power_W_median']} W" if args.clocks else ""), file=sys.stderr, flush=True)
+    print(json.dumps({"metric": "MFMA loops of a GEMM wave tile", "unit": "TFLOP/s",
+                      "workload": f"{grid} workgroups x {iters} iterations (64 of K) of the wave tile's MFMAs",
                       "peak": PEAK_BF16_TFLOPS, "results": res}), flush=True)
+
+
+def lds_patterns():
+    """Lane -> LDS byte offset tables of one ds_read_b128 (64 lanes): the operand layouts of
+    the GEMM kernels (rows of 64 K = 128 bytes; 32x32x16: lane l reads row l % 32, chunk
+    l / 32; 16x16x32: row l % 16, chunk l / 16) under their swizzles, and probes that put
+    two lanes differing in one index bit on the same bank at different addresses."""
+    swz = lambda r: (r ^ ((r >> 3) & 3)) & 7
+    far = lambda l: 16384 + 16 * l
+    pats = [("contiguous", [16 * l for l in range(64)]),
+            ("x32_swz", [(l % 32) * 128 + ((l // 32) ^ swz(l % 32)) * 16 for l in range(64)]),
+            ("x16_swz", [(l % 16) * 128 + ((l // 16) ^ swz(l % 16)) * 16 for l in range(64)]),
+            ("x16_rot", [(l % 16) * 128 + ((l // 16 + l % 16) % 8) * 16 for l in range(64)]),
+            ("x16_none", [(l % 16) * 128 + (l // 16) * 16 for l in range(64)]),
+            ("x16_swz_lanes0-15_only", [(l % 16) * 128 + ((l // 16) ^ swz(l % 16)) * 16 if l < 16 else far(l)
+                                        for l in range(64)]),
+            # rows of 32 K (64 bytes, 4 chunks; swizzle (r / 2 ^ (r >> 3) & 3) & 3), chunks 0-1 and 2-3
+            ("x32_k32_swz_c0", [(l % 32) * 64 + ((l // 32) ^ ((l % 32 // 2 ^ (l % 32 >> 3) & 3) & 3)) * 16
+                                for l in range(64)]),
+            ("x32_k32_swz_c2", [(l % 32) * 64 + ((2 + l // 32) ^ ((l % 32 // 2 ^ (l % 32 >> 3) & 3) & 3)) * 16
+                                for l in range(64)])]
+    for b in range(6):
+        pats.append((f"bit{b}_same_bank", [(l & ~(1 << b)) * 16 + ((l >> b) & 1) * 1024 for l in range(64)]))
+    return pats
+
+
+def bench_lds(args, torch):
+    """One launch per lane -> address pattern of lds_patterns() (t0mi_probe_lds: 256
+    workgroups x 8 waves x 2000 dependent ds_read_b128), in the order listed.  Under
+    rocprofv3 --pmc SQ_LDS_BANK_CONFLICT SQ_LDS_IDX_ACTIVE SQ_INSTS_LDS each dispatch's
+    counters give the LDS cycles per read of its pattern (4 when conflict-free)."""
+    from t0mi import probes
+    stream_ptr = torch.cuda.current_stream().cuda_stream
+    out = torch.empty(256 * 512, device="cuda:0", dtype=torch.int32)
+    res = []
+    for name, tab in lds_patterns():
+        t = torch.tensor(tab, dtype=torch.int32, device="cuda:0")
+        launch = lambda: probes.lds(stream_ptr, t.data_ptr(), 16, 2000, 256, out.data_ptr())
+        launch()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        launch()
+        torch.cuda.synchronize()
+        res.append({"name": name, "us_per_launch": round((time.perf_counter() - t0) * 1e6, 1)})
+        print(f"[bench] lds {len(res) - 1} {name}", file=sys.stderr, flush=True)
+    print(json.dumps({"metric": "LDS read patterns (ds_read_b128), one launch each, in order", "unit": "us",
+                      "patterns": res}), flush=True)
+
+
+def bench_vendor(args, torch, t0mi):
+    """torch.matmul (hipBLASLt on ROCm) against t0mi_gemm on BASELINE configs 2 and 3 and
+    the NT form of config 2, same operands (N(0,1) / N(0,0.02) bf16, bf16 out), same
+    timing (median of 5 event-timed batches on torch's current stream); B of config 3 is
+    rotated over 16 copies as in --only skinny."""
+    rt = t0mi.Runtime.on_torch_stream(0)
+    g = torch.Generator(device="cuda:0")
+    g.manual_seed(0x7801)
+    res = {}
+    cases = (("config2_4096_NN", 4096, 4096, 4096, 1.0, t0mi.NN, 1),
+             ("config2_4096_NT", 4096, 4096, 4096, 1.0, t0mi.NT, 1),
+             ("config3_128x4096x4096_NN", 128, 4096, 4096, 0.02, t0mi.NN, 16))
+    for name, m, n, k, sd, tr, copies in cases:
+        a = (torch.randn(m, k, device="cuda:0", generator=g) * sd).to(torch.bfloat16)
+        shape_b = (k, n) if tr == t0mi.NN else (n, k)
+        bs = [(torch.randn(*shape_b, device="cuda:0", generator=g) * sd).to(torch.bfloat16) for _ in range(copies)]
+        y = torch.empty(m, n, device="cuda:0", dtype=torch.bfloat16)
+        cfg = t0mi.auto_select_layout(m, k, n, tr, t0mi.OUT_BF16).copy(transpose=tr, out_dtype=t0mi.OUT_BF16)
+        pa, py = a.data_ptr(), y.data_ptr()
+        bp = [b.data_ptr() for b in bs]
+        ours = lambda i: rt.gemm(cfg, pa, bp[i % copies], py, m, n, k)
+        if tr == t0mi.NN:
+            theirs = lambda i: torch.matmul(a, bs[i % copies], out=y)
+        else:
+            bts = [b.t() for b in bs]  # a transposed view: torch picks the NT kernel
+            theirs = lambda i: torch.matmul(a, bts[i % copies], out=y)
+        row = {}
+        for who, fn in (("t0mi", ours), ("torch.matmul", theirs)):
+            warm_up(torch, lambda fn=fn: fn(0), args.warmup)
+            us, batches = timed_batches(torch, fn, max(args.steps, 2 * copies))
+            row[who] = {"us": round(us, 2), "TFLOP/s": round(2.0 * m * n * k / (us * 1e-6) / 1e12, 1),
+                        "batch_us": [round(b, 2) for b in batches]}
+        row["t0mi_kernel"] = cfg.name()
+        row["speedup"] = round(row["torch.matmul"]["us"] / row["t0mi"]["us"], 3)
+        res[name] = row
+        print(f"[bench] vendor {name}: t0mi {row['t0mi']['us']} us, torch.matmul {row['torch.matmul']['us']} us "
+              f"(x{row['speedup']})", file=sys.stderr, flush=True)
+    rt.close()
+    print(json.dumps({"metric": "t0mi_gemm vs torch.matmul (hipBLASLt), us per call", "unit": "us",
+                      "higher_is_better": False, "torch": torch.__version__, "results": res}), flush=True)
 
 
 def bench_dispatch(args, torch, t0mi):
@@ -611,9 +711,15 @@ def main():
     if args.only == "mfma":
         bench_mfma(args, torch)
         return
+    if args.only == "lds":
+        bench_lds(args, torch)
+        return
     import t0mi
     if args.only == "dispatch":
         bench_dispatch(args, torch, t0mi)
+        return
+    if args.only == "vendor":
+        bench_vendor(args, torch, t0mi)
         return
     rt = t0mi.Runtime.on_torch_stream(0)
     out = {"metric": METRIC, "n_gpus": 1, "steps": args.steps, "warmup": args.warmup, "higher_is_better": True,

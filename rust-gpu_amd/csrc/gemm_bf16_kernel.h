@@ -262,6 +262,78 @@ __device__ __forceinline__ void store_tile_bf16_staged(const GemmParams& p, cons
   }
 }
 
+// Stores one 16x16 accumulator block of v_mfma_f32_16x16x32_bf16: lane l holds
+// row m (= block row l % 16) and columns n .. n+3 (n already includes
+// 4*(l >> 4)).  Columns at or beyond N are skipped (the tile's N tail).
+__device__ __forceinline__ void store_block16(const GemmParams& p, const f32x4& a, char* ybase, int m, int n,
+                                              bool partial_plane) {
+  if (n >= (int)p.N) return;
+  float v0 = a[0], v1 = a[1], v2 = a[2], v3 = a[3];
+  if (!partial_plane && p.epi.n) {
+    f32x4 bv = {0.0f, 0.0f, 0.0f, 0.0f};
+    if (p.bias) bv = f32x4{p.bias[n], p.bias[n + 1], p.bias[n + 2], p.bias[n + 3]};
+    v0 = epi_apply(v0, bv.x, p.epi);
+    v1 = epi_apply(v1, bv.y, p.epi);
+    v2 = epi_apply(v2, bv.z, p.epi);
+    v3 = epi_apply(v3, bv.w, p.epi);
+  }
+  if (!partial_plane && p.out_bf16) {
+    u32x2 o;
+    o.x = pack_bf16x2(v0, v1);
+    o.y = pack_bf16x2(v2, v3);
+    *(u32x2*)((uint16_t*)ybase + (size_t)m * p.ldy + n) = o;
+  } else {
+    f32x4 o = {v0, v1, v2, v3};
+    *(f32x4*)((float*)ybase + (size_t)m * p.ldy + n) = o;
+  }
+}
+
+// store_tile_bf16_staged for a wave's FM*16 x 64 block of 16x16 accumulators
+// (FN = 4): each lane's 8-byte row pieces go to a private LDS block `st`
+// (FM*16 rows of 128 bytes, chunks swizzled by stage_swz16), which is read back
+// as 8 whole rows per 16-byte-per-lane store instruction.  Same contract.
+template <int FM>
+__device__ __forceinline__ void store_tile_bf16_staged16(const GemmParams& p, const f32x4 (&acc)[4][FM], char* st,
+                                                         char* ybase, int row0, int col0, int lane) {
+  constexpr int TN = 64, CH = 8, RPI = 8;  // 16-byte chunks per row, rows per store instruction
+  const int lr = lane & 15, lq = lane >> 4;
+  static_for<FM>([&](auto fmc) {
+    constexpr int fm = decltype(fmc)::value;
+    const int r = fm * 16 + lr;
+    static_for<4>([&](auto fnc) {
+      constexpr int fn = decltype(fnc)::value;
+      float v0 = acc[fn][fm][0], v1 = acc[fn][fm][1], v2 = acc[fn][fm][2], v3 = acc[fn][fm][3];
+      if (p.epi.n) {
+        const int nc = col0 + fn * 16 + lq * 4;
+        f32x4 bv = {0.0f, 0.0f, 0.0f, 0.0f};
+        if (p.bias) bv = f32x4{p.bias[nc], p.bias[nc + 1], p.bias[nc + 2], p.bias[nc + 3]};
+        v0 = epi_apply(v0, bv.x, p.epi);
+        v1 = epi_apply(v1, bv.y, p.epi);
+        v2 = epi_apply(v2, bv.z, p.epi);
+        v3 = epi_apply(v3, bv.w, p.epi);
+      }
+      const int c = fn * 2 + (lq >> 1);  // 16-byte chunk of the row
+      u32x2 o;
+      o.x = pack_bf16x2(v0, v1);
+      o.y = pack_bf16x2(v2, v3);
+      *(u32x2*)(st + r * TN * 2 + ((c ^ stage_swz16(r)) * 16) + (lq & 1) * 8) = o;
+    });
+  });
+  wait_lgkmcnt0();  // the block is read back only by the wave that wrote it
+  const int rr = lane / CH, cc = lane % CH;
+  char* yrow = ybase + ((size_t)(row0 + rr) * p.ldy + col0 + cc * 8) * 2;
+#pragma unroll
+  for (int i = 0; i < FM * 16 / RPI; ++i) {
+    const int r = i * RPI + rr;
+    const u32x4 v = *(const u32x4*)(st + r * TN * 2 + ((cc ^ stage_swz16(r)) * 16));
+    u32x4* dst = (u32x4*)(yrow + (size_t)i * RPI * p.ldy * 2);
+    if (p.stream_out)
+      __builtin_nontemporal_store(v, dst);
+    else
+      *dst = v;
+  }
+}
+
 template <int BM, int BN, int BK, int WM, int WN, int S, bool NN>
 struct GemmTile {
   static constexpr int NWAVES = WM * WN;

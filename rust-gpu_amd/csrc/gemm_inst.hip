@@ -19,7 +19,7 @@ template <int BM, int BN, int BK, int WM, int WN, int S, bool NN>
 static void launch_variant(dim3 g, hipStream_t s, const GemmParams& p) {
   if constexpr (BM == 256 && BN == 256 && BK == 64 && WM == 2 && WN == 4 && S == 2) {
     if (pingpong_ok(p)) {
-      hipLaunchKernelGGL(gemm_bf16_pingpong_kernel<NN>, g, dim3(512), 0, s, p);
+      hipLaunchKernelGGL((gemm_bf16_pingpong_kernel<NN, true>), g, dim3(512), 0, s, p);
       return;
     }
   }

@@ -6,10 +6,11 @@
 //     bytes once can do, and the calibration of rocprofv3 FETCH_SIZE for that
 //     load type;
 //   - an empty kernel: the per-launch cost of back-to-back dispatches;
-//   - a pure MFMA loop (v_mfma_f32_32x32x16_bf16, the GEMM's instruction, in
-//     the ping-pong kernel's per-phase pattern) on random or zero operands,
-//     with s_memtime / s_memrealtime stamps: the FLOP rate and the shader clock
-//     the power limit allows with no memory traffic at all.
+//   - MFMA loops (32x32x16 or 16x16x32 bf16, with the register set of a GEMM
+//     wave tile of 128 x 64 or 128 x 128, operands in registers or re-read from
+//     LDS) on random or zero operands, with s_memtime / s_memrealtime stamps:
+//     the FLOP rate and the shader clock the power limit allows with no HBM
+//     traffic, and what the LDS reads of each wave tile cost in clock.
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
@@ -18,6 +19,7 @@ namespace {
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 
 // Each thread reads UNROLL 16-byte elements per step, `stride` elements apart,
 // and folds them with XOR; a workgroup stores its fold only if it equals a
@@ -72,46 +74,96 @@ __global__ __launch_bounds__(256) void probe_empty(uint32_t never, uint32_t* sin
   if (threadIdx.x == never) sink[0] = never;
 }
 
-// 8 waves (two per SIMD), each with the ping-pong kernel's register set: 16 A
-// and 8 B fragments (4 k-steps of 4 x 2 fragments) and 8 accumulators of
-// 32x32; one iteration = the 32 MFMAs of a 64-K tile.  Wave 0 of each
-// workgroup records (s_memtime, s_memrealtime) before and after its loop.
-__global__ __launch_bounds__(512) void probe_mfma(const bf16x8* __restrict__ src, uint32_t n_frag, uint32_t iters,
-                                                  float* __restrict__ out, uint64_t* __restrict__ stamps) {
-  bf16x8 xa[4][4], xb[4][2];
-  const uint32_t t = blockIdx.x * 512 + threadIdx.x;
-#pragma unroll
-  for (int ks = 0; ks < 4; ++ks) {
-#pragma unroll
-    for (int f = 0; f < 4; ++f) xa[ks][f] = src[(t * 24 + ks * 6 + f) % n_frag];
-#pragma unroll
-    for (int f = 0; f < 2; ++f) xb[ks][f] = src[(t * 24 + ks * 6 + 4 + f) % n_frag];
+// MFMA loop with a GEMM wave's register set.  WAVES waves per workgroup (8: two
+// per SIMD, 4: one), each owning FM x FN accumulator blocks and running, per
+// iteration (64 of K), the blocks' MFMAs in k-step order:
+//   X16 = false: v_mfma_f32_32x32x16_bf16, 4 k-steps of 16, blocks 32 x 32;
+//   X16 = true:  v_mfma_f32_16x16x32_bf16, 2 k-steps of 32, blocks 16 x 16.
+// LDS = false: the fragments stay in registers (loaded once); LDS = true: every
+// k-step's fragments are read from LDS (64 KB of src copied in at the start,
+// ds_read_b128 of whole 1 KB blocks, conflict-free), one k-step ahead, one read
+// after each of the step's first FM + FN MFMAs, waited for at the start of the
+// next step -- the LDS traffic of a GEMM with that wave tile.  Wave 0 of each workgroup records (s_memtime,
+// s_memrealtime) before and after its loop.
+template <int WAVES, int FM, int FN, bool X16, bool LDS>
+__global__ __launch_bounds__(WAVES * 64) void probe_mfma(const bf16x8* __restrict__ src, uint32_t n_frag,
+                                                         uint32_t iters, float* __restrict__ out,
+                                                         uint64_t* __restrict__ stamps) {
+  constexpr int KS = X16 ? 2 : 4, NF = FM + FN;
+  typedef float accv __attribute__((ext_vector_type(X16 ? 4 : 16)));
+  __shared__ __attribute__((aligned(1024))) bf16x8 lds[LDS ? 4096 : 1];
+  const uint32_t t = blockIdx.x * (WAVES * 64) + threadIdx.x;
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+  if constexpr (LDS) {
+    for (uint32_t c = threadIdx.x; c < 4096; c += WAVES * 64) lds[c] = src[(blockIdx.x * 4096u + c) % n_frag];
   }
-  f32x16 acc[2][4];
+  // registers: without LDS all KS steps' fragments; with LDS two steps' (current, next)
+  constexpr int RS = LDS ? 2 : KS;
+  bf16x8 x[RS][NF];
+  // block of fragment (ks, f) in iteration it: a per-iteration base below 32
+  // plus ks * NF + f (< 32), so each read is one ds_read_b128 with a constant offset
+  auto lds_frag = [&](uint32_t it, int ks, int f) {
+    const int base = (int)((it * 5u + (uint32_t)wave * 7u) & 31u);
+    return lds[(base + ks * NF + f) * 64 + lane];
+  };
+  if constexpr (!LDS) {
 #pragma unroll
-  for (int fn = 0; fn < 2; ++fn)
+    for (int ks = 0; ks < KS; ++ks)
 #pragma unroll
-    for (int fm = 0; fm < 4; ++fm)
+      for (int f = 0; f < NF; ++f) x[ks][f] = src[(t * (KS * NF) + ks * NF + f) % n_frag];
+  }
+  accv acc[FN][FM];
 #pragma unroll
-      for (int r = 0; r < 16; ++r) acc[fn][fm][r] = 0.0f;
+  for (int fn = 0; fn < FN; ++fn)
+#pragma unroll
+    for (int fm = 0; fm < FM; ++fm)
+#pragma unroll
+      for (int r = 0; r < (X16 ? 4 : 16); ++r) acc[fn][fm][r] = 0.0f;
   __syncthreads();
+  if constexpr (LDS) {
+#pragma unroll
+    for (int f = 0; f < NF; ++f) x[0][f] = lds_frag(0, 0, f);
+  }
   const uint64_t c0 = __builtin_amdgcn_s_memtime(), r0 = __builtin_amdgcn_s_memrealtime();
   for (uint32_t it = 0; it < iters; ++it) {
 #pragma unroll
-    for (int ks = 0; ks < 4; ++ks)
+    for (int ks = 0; ks < KS; ++ks) {
+      const int cur = LDS ? (ks & 1) : ks, nxt = (ks + 1) & 1;
+      const uint32_t nit = ks + 1 < KS ? it : it + 1;
+      const int nks = ks + 1 < KS ? ks + 1 : 0;
+      // this step's fragments (read during the previous step) have landed; the
+      // next step's reads all follow
+      if constexpr (LDS) __builtin_amdgcn_s_waitcnt(0xF | (0x7 << 4) | (0x3 << 14));
+      __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-      for (int fn = 0; fn < 2; ++fn)
+      for (int i = 0; i < FN * FM; ++i) {
+        const int fn = i / FM, fm = i % FM;
+        if constexpr (X16)
+          acc[fn][fm] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(x[cur][FM + fn], x[cur][fm], acc[fn][fm], 0, 0, 0);
+        else
+          acc[fn][fm] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(x[cur][FM + fn], x[cur][fm], acc[fn][fm], 0, 0, 0);
+        if constexpr (LDS) {
+          if (i < NF) x[nxt][i] = lds_frag(nit, nks, i);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+      }
+      // Keep this step's fragments live to the end of the step, so the next
+      // step's reads cannot be given the registers of fragments that MFMAs
+      // still in flight are reading.
+      if constexpr (LDS) {
 #pragma unroll
-        for (int fm = 0; fm < 4; ++fm)
-          acc[fn][fm] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(xb[ks][fn], xa[ks][fm], acc[fn][fm], 0, 0, 0);
+        for (int f = 0; f < NF; ++f) asm volatile("" ::"v"(x[cur][f]));
+      }
+    }
   }
   float s = 0.0f;
 #pragma unroll
-  for (int fn = 0; fn < 2; ++fn)
+  for (int fn = 0; fn < FN; ++fn)
 #pragma unroll
-    for (int fm = 0; fm < 4; ++fm)
+    for (int fm = 0; fm < FM; ++fm)
 #pragma unroll
-      for (int r = 0; r < 16; ++r) s += acc[fn][fm][r];
+      for (int r = 0; r < (X16 ? 4 : 16); ++r) s += acc[fn][fm][r];
   const uint64_t c1 = __builtin_amdgcn_s_memtime(), r1 = __builtin_amdgcn_s_memrealtime();
   out[t] = s;
   if (threadIdx.x == 0) {
@@ -120,6 +172,35 @@ __global__ __launch_bounds__(512) void probe_mfma(const bf16x8* __restrict__ src
     stamps[4 * blockIdx.x + 2] = r0;
     stamps[4 * blockIdx.x + 3] = r1;
   }
+}
+
+// LDS read pattern: every wave of the workgroup reads, iters times, 16 bytes
+// (ds_read_b128) or 8 bytes (ds_read_b64) per lane at byte offset table[lane]
+// of a 64 KB LDS buffer, one read in flight per wave.  Run under rocprofv3
+// with SQ_LDS_BANK_CONFLICT / SQ_LDS_IDX_ACTIVE, a table tells how many LDS
+// cycles one read of that lane -> address pattern takes.
+template <int BYTES>
+__global__ __launch_bounds__(512) void probe_lds(const uint32_t* __restrict__ table, uint32_t iters,
+                                                 uint32_t* __restrict__ out) {
+  __shared__ __attribute__((aligned(1024))) u32x4 lds[4096];
+  for (uint32_t c = threadIdx.x; c < 4096; c += 512) lds[c] = u32x4{c, c + 1u, c + 2u, c + 3u};
+  __syncthreads();
+  const uint32_t off = table[threadIdx.x & 63] & 0xFFF8u;
+  const uint32_t addr = (uint32_t)(size_t)(const __attribute__((address_space(3))) void*)lds + off;
+  u32x4 acc = {0u, 0u, 0u, 0u};
+  for (uint32_t it = 0; it < iters; ++it) {
+    u32x4 v = {0u, 0u, 0u, 0u};
+    if constexpr (BYTES == 16) {
+      asm volatile("ds_read_b128 %0, %1\n\ts_waitcnt lgkmcnt(0)" : "=v"(v) : "v"(addr));
+    } else {
+      u32x2 w;
+      asm volatile("ds_read_b64 %0, %1\n\ts_waitcnt lgkmcnt(0)" : "=v"(w) : "v"(addr));
+      v.x = w.x;
+      v.y = w.y;
+    }
+    acc ^= v;
+  }
+  out[blockIdx.x * 512 + threadIdx.x] = acc.x ^ acc.y ^ acc.z ^ acc.w;
 }
 
 int launched() { return hipGetLastError() == hipSuccess ? 0 : -3; }
@@ -163,15 +244,56 @@ int t0mi_probe_empty(void* stream, uint32_t grid, uint32_t* sink) {
   return launched();
 }
 
-// `grid` workgroups of 8 waves, each wave running iters x 32 MFMAs 32x32x16
-// (2 * 32 * 32 * 16 * 32 FLOP per iteration) on fragments taken from src
-// (n_frag 16-byte fragments).  out: grid * 512 floats; stamps: grid * 4 u64.
+// `grid` workgroups running the MFMA loop `variant` for `iters` iterations
+// (64 of K each) on fragments taken from src (n_frag 16-byte fragments):
+//   0: 8 waves x (4 x 2 blocks 32x32x16), registers only (the ping-pong
+//      GEMM's wave tile, 128 x 64);   1: the same, fragments read from LDS;
+//   2: 4 waves x (4 x 4 blocks 32x32x16) (wave tile 128 x 128);  3: + LDS;
+//   4: 4 waves x (8 x 8 blocks 16x16x32) (wave tile 128 x 128);  5: + LDS;
+//   6: 8 waves x (8 x 4 blocks 16x16x32) (wave tile 128 x 64);   7: + LDS.
+// Each SIMD runs 2^21 FLOP per iteration in every variant (a workgroup's
+// count: t0mi_probe_mfma_flop).  out: grid * 512 floats; stamps: grid * 4 u64.
 int t0mi_probe_mfma(void* stream, const void* src, uint32_t n_frag, uint32_t iters, uint32_t grid, float* out,
-                    uint64_t* stamps) {
+                    uint64_t* stamps, int variant) {
   if (!src || !out || !stamps || n_frag == 0 || grid == 0 || ((uintptr_t)src & 15)) return -1;
-  hipLaunchKernelGGL(probe_mfma, dim3(grid), dim3(512), 0, (hipStream_t)stream, (const bf16x8*)src, n_frag, iters,
-                     out, stamps);
+  const hipStream_t st = (hipStream_t)stream;
+  const bf16x8* s = (const bf16x8*)src;
+  switch (variant) {
+    case 0: hipLaunchKernelGGL((probe_mfma<8, 4, 2, false, false>), dim3(grid), dim3(512), 0, st, s, n_frag, iters, out, stamps); break;
+    case 1: hipLaunchKernelGGL((probe_mfma<8, 4, 2, false, true>), dim3(grid), dim3(512), 0, st, s, n_frag, iters, out, stamps); break;
+    case 2: hipLaunchKernelGGL((probe_mfma<4, 4, 4, false, false>), dim3(grid), dim3(256), 0, st, s, n_frag, iters, out, stamps); break;
+    case 3: hipLaunchKernelGGL((probe_mfma<4, 4, 4, false, true>), dim3(grid), dim3(256), 0, st, s, n_frag, iters, out, stamps); break;
+    case 4: hipLaunchKernelGGL((probe_mfma<4, 8, 8, true, false>), dim3(grid), dim3(256), 0, st, s, n_frag, iters, out, stamps); break;
+    case 5: hipLaunchKernelGGL((probe_mfma<4, 8, 8, true, true>), dim3(grid), dim3(256), 0, st, s, n_frag, iters, out, stamps); break;
+    case 6: hipLaunchKernelGGL((probe_mfma<8, 8, 4, true, false>), dim3(grid), dim3(512), 0, st, s, n_frag, iters, out, stamps); break;
+    case 7: hipLaunchKernelGGL((probe_mfma<8, 8, 4, true, true>), dim3(grid), dim3(512), 0, st, s, n_frag, iters, out, stamps); break;
+    default: return -1;
+  }
   return launched();
+}
+
+// `grid` workgroups of 8 waves reading LDS with the lane -> byte offset
+// pattern table[0..63] (device memory; offsets below 64 KB, multiples of the read size),
+// `iters` reads per wave of `bytes` (16 or 8) per lane.  out: grid * 512 u32.
+int t0mi_probe_lds(void* stream, const uint32_t* table, uint32_t bytes, uint32_t iters, uint32_t grid,
+                   uint32_t* out) {
+  if (!table || !out || grid == 0 || (bytes != 16 && bytes != 8)) return -1;
+  if (bytes == 16)
+    hipLaunchKernelGGL(probe_lds<16>, dim3(grid), dim3(512), 0, (hipStream_t)stream, table, iters, out);
+  else
+    hipLaunchKernelGGL(probe_lds<8>, dim3(grid), dim3(512), 0, (hipStream_t)stream, table, iters, out);
+  return launched();
+}
+
+// FLOP one workgroup of MFMA-loop `variant` runs per iteration (0 for an unknown variant).
+uint64_t t0mi_probe_mfma_flop(int variant) {
+  switch (variant) {
+    case 0: case 1: return 8ull * 8 * 4 * (2 * 32 * 32 * 16);
+    case 2: case 3: return 4ull * 16 * 4 * (2 * 32 * 32 * 16);
+    case 4: case 5: return 4ull * 64 * 2 * (2 * 16 * 16 * 32);
+    case 6: case 7: return 8ull * 32 * 2 * (2 * 16 * 16 * 32);
+    default: return 0;
+  }
 }
 
 }  // extern "C"

@@ -52,8 +52,9 @@ def test_leg_prints_one_json_line(leg, unit, bound):
 
 @pytest.mark.gpu
 def test_probe_floors_print_one_json_line():
-    """--only stream / mfma (libt0mi_probes.so): the decode's streaming-read and empty-launch
-    floors, and the pure-MFMA rate with its shader clock."""
+    """--only stream / mfma / lds (libt0mi_probes.so): the decode's streaming-read and
+    empty-launch floors, the MFMA loops' rates with their shader clocks, and the LDS
+    bank-pattern launches."""
     r = run_bench("--only", "stream", "--steps", "12", "--warmup", "2")
     assert r.returncode == 0, r.stderr[-2000:]
     out = json.loads(r.stdout.strip().splitlines()[-1])
@@ -62,5 +63,11 @@ def test_probe_floors_print_one_json_line():
     r = run_bench("--only", "mfma", "--steps", "2", "--warmup", "1")
     assert r.returncode == 0, r.stderr[-2000:]
     res = json.loads(r.stdout.strip().splitlines()[-1])["results"]
-    for name in ("random", "zero"):
-        assert 0 < res[name]["frac_of_peak"] < 1.05 and 100 < res[name]["shader_clock_MHz_median"] < 3000
+    assert {"v0_zero", "v0_random", "v5_random", "v7_random"} <= set(res)
+    for v in res.values():
+        assert 0 < v["frac_of_peak"] < 1.05 and 100 < v["shader_clock_MHz_median"] < 3000
+    r = run_bench("--only", "lds")
+    assert r.returncode == 0, r.stderr[-2000:]
+    out = json.loads(r.stdout.strip().splitlines()[-1])
+    assert [p["name"] for p in out["patterns"]][:3] == ["contiguous", "x32_swz", "x16_swz"]
+    assert all(p["us_per_launch"] > 0 for p in out["patterns"])

@@ -1,9 +1,12 @@
 """CPU simulation of the gfx950 kernels' index maps (tests/index_maps_sim.cpp, built
 with g++ from rust-gpu_amd/csrc/index_maps.h — the header the kernels include):
 DMA coverage exactly once, LDS bijections, fragment reads finding the chunk the
-MFMA expects, the ping-pong kernel's hoisted per-wave offsets, the W4A16 decode
-slot map, and bank-conflict freedom of the swizzles.  The counterpart of the
-reference's pure-CPU locks in tests/gemm_memory_safety.rs."""
+MFMA expects (32x32x16 and 16x16x32 operand layouts, the 16x16x32 transpose-read
+lane map), the ping-pong kernel's hoisted per-wave offsets, the W4A16 decode slot
+map, and bank-conflict freedom of the swizzles under every LDS bank rule that
+reproduces the conflict counts measured on gfx950 (the measured cycles per read of
+the probe patterns are data in the simulation).  The counterpart of the reference's
+pure-CPU locks in tests/gemm_memory_safety.rs."""
 import os
 import shutil
 import subprocess
@@ -20,4 +23,6 @@ def test_index_maps_simulation(tmp_path):
                     os.path.join(HERE, "index_maps_sim.cpp")], check=True)
     r = subprocess.run([exe], capture_output=True, text=True, timeout=120)
     assert r.returncode == 0, r.stdout[-4000:]
-    assert " 0 failures" in r.stdout and int(r.stdout.split()[0]) > 100000, r.stdout
+    lines = r.stdout.strip().splitlines()
+    assert int(lines[0].split()[0]) > 0, r.stdout  # LDS bank rules that fit the measurements
+    assert lines[-1].endswith(" 0 failures") and int(lines[-1].split()[0]) > 100000, r.stdout
