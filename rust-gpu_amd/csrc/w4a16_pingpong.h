@@ -8,9 +8,15 @@
 // 4e..4e+3, the reference's low-nibble-first order, src/t0/quant_kernels.rs:3-10),
 // scales bf16 [K/g][N], zero points packed int4 u32 [K/g][N/8] or a constant.
 // The weight is rounded once to bf16, exactly as dequant_int4_kernel does for
-// the dequant-then-GEMM route, and the MFMA order per accumulator is that of
-// gemm_bf16_pingpong_kernel<NN, true> (v_mfma_f32_16x16x32_bf16, 8 x 4 blocks
-// per wave): for the same problem the two routes give bit-identical results.
+// the dequant-then-GEMM route, and each accumulator sums its products in the
+// same k order as gemm_bf16_pingpong_kernel<NN, true>: for the same problem the
+// two routes give bit-identical results (that kernel issues
+// v_mfma_f32_16x16x32_bf16, this one v_mfma_f32_32x32x16_bf16, which on gfx950
+// give identical sums for the same k order; the GPU tests check it).  This
+// kernel stays on 32x32x16: with 16x16x32 blocks its read phase (8 packed words,
+// the scales and zero points of 4 column blocks and the dequant temporaries)
+// no longer fits beside the 128 accumulators and 96 operand registers of the
+// 256 a wave has, and spills.
 //
 // What differs from the bf16 GEMM: the B tile is DMA'd as packed words (8 rows
 // of 256 words = 8 KB per 64-K tile instead of 32 KB of bf16).  In the NN MFMA
@@ -19,9 +25,8 @@
 // instructions in the read phase: nibbles spread to bytes (2 AND/shift),
 // v_cvt_f32_ubyte0..3, one fma q*s + (-z*s) (exact: |q - z| < 16 and s has 8
 // significant bits) and v_cvt_pk_bf16_f32 (RNE).  The read phase has the slack
-// for it and for the DMA (the MFMA phase is the longer of the two).  Each
-// tile's 256 scales and 32 zero words travel with its packed words (DMA into
-// the same LDS slot).
+// for it (the MFMA phase is the longer of the two).  Each tile's 256 scales
+// and 32 zero words travel with its packed words (DMA into the same LDS slot).
 //
 // Preconditions (w4_pingpong_ok): K and the split-K partition length are
 // multiples of 64 and the group a multiple of 64, so every 64-K tile lies in
@@ -79,15 +84,14 @@ template <bool ZEROS>
 __global__ __launch_bounds__(512) void w4a16_pingpong_kernel(W4PPParams q) {
   const GemmParams& p = q.g;
   constexpr int BK = 64, TN = 64;
-  constexpr int FM = 8, FN = 4, KC = 8, KS = 2;  // 16x16 blocks per wave, k-steps of 32
-  constexpr int AH_BYTES = 128 * BK * 2;         // half A tile, bf16
-  // Packed-word B tile: 8 k-octet rows of 256 words, rows BROW bytes apart; a
-  // fragment read takes 16 consecutive words of each of 4 consecutive rows
-  // (lane l: row 4 ks + l / 16), and a pitch of 272 words (16 mod 64 banks)
-  // puts those four runs on disjoint banks.  Then the tile's 256 bf16 scales
-  // (at +0 of the SZ area) and 32 zero words (at +1024); the rest of the SZ
-  // area takes the zeros that the out-of-range lanes of those two DMAs write.
-  constexpr int BROW = 1088, SZ = 8 * BROW, BSLOT = SZ + 2048;
+  constexpr int FM = 4, FN = 2, KC = 8, KS = 4;
+  constexpr int AH_BYTES = 128 * BK * 2;  // half A tile, bf16
+  // Packed-word B tile: 8 k-octet rows of 256 words, rows 1152 bytes apart so
+  // that the two half-waves of a fragment read (rows kk, kk+1) hit disjoint
+  // banks; then the tile's 256 bf16 scales (at +0 of the SZ area) and 32 zero
+  // words (at +1024); the rest of the SZ area takes the zeros that the
+  // out-of-range lanes of those two DMAs write.
+  constexpr int BROW = 1152, SZ = 8 * BROW, BSLOT = SZ + 2048;
   constexpr int A_AREA = 4 * AH_BYTES;  // two groups x two slots
   constexpr int LDS_BYTES = A_AREA + 3 * BSLOT > 8 * 16384 ? A_AREA + 3 * BSLOT : 8 * 16384;  // staged store reuses it
   __shared__ __attribute__((aligned(1024))) uint8_t smem[LDS_BYTES];
@@ -110,13 +114,11 @@ __global__ __launch_bounds__(512) void w4a16_pingpong_kernel(W4PPParams q) {
   const uint32_t b_lds0 = smem_base + (uint32_t)A_AREA + (uint32_t)((4 * g + w4) * BROW);
 
   // ---- DMA -----------------------------------------------------------------
-  // A: as in gemm_bf16_pingpong_kernel<., true> (four row-block resources per
-  // group, the 16x16x32 row layout).
+  // A: four row-block resources per group, as in gemm_bf16_pingpong_kernel.
   uint32_t a_voff;
   {
-    int row, lc;
-    kc_dma_chunk<KC, true>(w4 * 64 + lane, &row, &lc);
-    a_voff = (uint32_t)(row * (int)p.lda + lc * 8) * 2u;
+    const int row = w4 * 8 + (lane >> 3), pc = lane & 7;
+    a_voff = (uint32_t)(row * (int)p.lda + ((pc ^ swz<KC>(row)) * 8)) * 2u;
   }
   const uint64_t a_row_bytes = (uint64_t)p.lda * 2u;
   u32x4 a_rs[4];
@@ -143,7 +145,6 @@ __global__ __launch_bounds__(512) void w4a16_pingpong_kernel(W4PPParams q) {
   };
   // Scales (and zero words) of tile t: 512 (128) bytes from column n0 of the
   // tile's group row, issued by wave 0; lanes past them are out of range.
-  constexpr int NSZ = ZEROS ? 2 : 1;  // wave 0's extra loads per tile
   auto dma_sz = [&](int t) {
     const uint32_t gk = (uint32_t)(kbeg + t * BK) / q.group;
     const uint32_t slot = smem_base + (uint32_t)A_AREA + (uint32_t)((t % 3) * BSLOT) + SZ;
@@ -158,54 +159,42 @@ __global__ __launch_bounds__(512) void w4a16_pingpong_kernel(W4PPParams q) {
                      (uint32_t)lane * 16u, 0u, slot + 1024u);
     }
   };
-  // s_waitcnt vmcnt(N) with N = n for waves 1-7 and n + extra for wave 0.
-  auto wait_loads = [&](auto n_c, auto extra_c) {
-    constexpr int n = decltype(n_c)::value, extra = decltype(extra_c)::value;
-    if (wave == 0)
-      wait_vmcnt<n + extra>();
-    else
-      wait_vmcnt<n>();
-  };
+  constexpr int NDMA = 5;
 
-  const int lr = lane & 15, lq = lane >> 4;
+  const int lrow = lane & 31, lhalf = lane >> 5;
   // ---- LDS -> fragments --------------------------------------------------------
   int a_off[KS];
 #pragma unroll
-  for (int ks = 0; ks < KS; ++ks) a_off[ks] = kc_slot<KC, true>(lr, ks * 4 + lq) * 8;
+  for (int ks = 0; ks < KS; ++ks) a_off[ks] = lrow * BK + (((ks * 2 + lhalf) ^ swz<KC>(lrow)) * 8);
   bf16x8 xa[KS][FM], xb[KS][FN];
   uint32_t bw[KS][FN];
   // A fragment i (k-step i / FM, row block i % FM); B word i (k-step i / FN,
-  // column block i % FN): k-octet row 4 ks + l / 16, column 16 fn + l % 16 of
-  // the wave's 64.
+  // column block i % FN).
   auto read_a = [&](const uint16_t* As, auto ic) {
     constexpr int i = decltype(ic)::value;
-    xa[i / FM][i % FM] = *(const bf16x8*)(As + a_off[i / FM] + (i % FM) * 16 * BK);
+    xa[i / FM][i % FM] = *(const bf16x8*)(As + a_off[i / FM] + (i % FM) * 32 * BK);
   };
-  const int b_lane = lq * (BROW / 4) + wn * TN + lr;  // in words
+  // B word of k-step ks, column block fn: a lane base plus an immediate.
+  const int b_lane = lhalf * (BROW / 4) + wn * TN + lrow;  // in words
   auto read_b = [&](const uint32_t* Bw, auto ic) {
     constexpr int i = decltype(ic)::value;
     constexpr int ks = i / FN, fn = i % FN;
-    bw[ks][fn] = Bw[b_lane + ks * 4 * (BROW / 4) + fn * 16];
+    bw[ks][fn] = Bw[b_lane + ks * 2 * (BROW / 4) + fn * 32];
   };
 
-  f32x4 acc[FN][FM];
+  f32x16 acc[FN][FM];
 #pragma unroll
   for (int fn = 0; fn < FN; ++fn)
 #pragma unroll
     for (int fm = 0; fm < FM; ++fm)
 #pragma unroll
-      for (int r = 0; r < 4; ++r) acc[fn][fm][r] = 0.0f;
+      for (int r = 0; r < 16; ++r) acc[fn][fm][r] = 0.0f;
 
   const uint16_t* a_slots = (const uint16_t*)(smem + g * 2 * AH_BYTES);
   // R(u): tile u's 8 packed B words and its scales / zero points, then its 16
   // A fragments with one word dequantized after every second A read, so the
-  // VALU work overlaps the A reads in flight and each word dies early.  The
-  // DMA of this wave (A of tile u+1 when DA; B, and for wave 0 the scales and
-  // zero points, of tile u+2 when DB) is issued between the A reads; at the end
-  // every load issued before R(u) is waited for (B of tile u+1, which the other
-  // group reads after the next barrier).
-  auto read_phase = [&](int u, auto da_c, auto db_c) {
-    constexpr bool DA = decltype(da_c)::value, DB = decltype(db_c)::value;
+  // VALU work overlaps the A reads in flight and each word dies early.
+  auto read_phase = [&](int u) {
     const uint16_t* As = a_slots + (u & 1) * (AH_BYTES / 2);
     const uint8_t* Bslot = smem + A_AREA + (u % 3) * BSLOT;
     const uint32_t* Bw = (const uint32_t*)Bslot;
@@ -213,19 +202,19 @@ __global__ __launch_bounds__(512) void w4a16_pingpong_kernel(W4PPParams q) {
       read_b(Bw, ic);
       __builtin_amdgcn_sched_barrier(0);
     });
-    float s_t[FN], cz_t[FN];
-    uint32_t sraw[FN], zraw[FN];
+    float s_t[2], cz_t[2];
+    uint32_t sraw[2], zraw[2];
 #pragma unroll
-    for (int f = 0; f < FN; ++f) {
-      sraw[f] = ((const uint16_t*)(Bslot + SZ))[wn * TN + f * 16 + lr];
-      if constexpr (ZEROS) zraw[f] = ((const uint32_t*)(Bslot + SZ + 1024))[(wn * TN + f * 16 + lr) / 8];
+    for (int f = 0; f < 2; ++f) {
+      sraw[f] = ((const uint16_t*)(Bslot + SZ))[wn * TN + f * 32 + lrow];
+      if constexpr (ZEROS) zraw[f] = ((const uint32_t*)(Bslot + SZ + 1024))[(wn * TN + f * 32 + lrow) / 8];
     }
     __builtin_amdgcn_sched_barrier(0);
     wait_lgkmcnt0();
 #pragma unroll
-    for (int f = 0; f < FN; ++f) {
+    for (int f = 0; f < 2; ++f) {
       s_t[f] = __builtin_bit_cast(float, sraw[f] << 16);
-      const float z = ZEROS ? (float)((zraw[f] >> (4 * (lr & 7))) & 0xFu) : (float)q.zp_const;
+      const float z = ZEROS ? (float)((zraw[f] >> (4 * (lrow & 7))) & 0xFu) : (float)q.zp_const;
       cz_t[f] = -z * s_t[f];  // exact: z < 16, s has 8 significant bits
     }
     static_for<KS * FM>([&](auto ic) {
@@ -235,27 +224,22 @@ __global__ __launch_bounds__(512) void w4a16_pingpong_kernel(W4PPParams q) {
         constexpr int wi = i / 2, ks = wi / FN, fn = wi % FN;
         xb[ks][fn] = dequant_word(bw[ks][fn], s_t[fn], cz_t[fn]);
       }
-      if constexpr (DA && i % 2 == 1 && i / 2 < 4) dma(u + 1, std::integral_constant<int, i / 2>{});
-      if constexpr (DB && i == 9) dma(u + 2, std::integral_constant<int, 4>{});
-      if constexpr (DB && i == 11)
-        if (wave == 0) dma_sz(u + 2);
       __builtin_amdgcn_sched_barrier(0);
     });
     wait_lgkmcnt0();
-    wait_loads(std::integral_constant<int, (DA ? 4 : 0) + (DB ? 1 : 0)>{},
-               std::integral_constant<int, DB ? NSZ : 0>{});
   };
-  // M(u): the tile's MFMAs in k-step order, then this wave's A of tile u+1 is
-  // waited for (its B, scales and zero points of tile u+2 may stay in flight).
-  auto mfma_phase = [&](auto db_c) {
-    constexpr bool DB = decltype(db_c)::value;
+  auto mfma_phase = [&](auto dma_c, int td) {
+    constexpr bool D = decltype(dma_c)::value;
     static_for<KS * FN * FM>([&](auto ic) {
       constexpr int i = decltype(ic)::value;
       constexpr int ks = i / (FN * FM), fn = (i / FM) % FN, fm = i % FM;
-      acc[fn][fm] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xb[ks][fn], xa[ks][fm], acc[fn][fm], 0, 0, 0);
+      acc[fn][fm] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(xb[ks][fn], xa[ks][fm], acc[fn][fm], 0, 0, 0);
+      if constexpr (D && i >= 16 && (i - 16) % 3 == 0 && (i - 16) / 3 < NDMA)
+        dma(td, std::integral_constant<int, (i - 16) / 3>{});
+      if constexpr (D && i == 31)
+        if (wave == 0) dma_sz(td);
       __builtin_amdgcn_sched_barrier(0);
     });
-    wait_loads(std::integral_constant<int, DB ? 1 : 0>{}, std::integral_constant<int, DB ? NSZ : 0>{});
   };
   auto bar = []() {
     __builtin_amdgcn_sched_barrier(0);
@@ -265,58 +249,54 @@ __global__ __launch_bounds__(512) void w4a16_pingpong_kernel(W4PPParams q) {
   using True = std::integral_constant<bool, true>;
   using False = std::integral_constant<bool, false>;
 
-  // The schedule of gemm_bf16_pingpong_kernel: R(u) bar M(u) bar per tile,
-  // group 1 one barrier behind; the prologue loads tile 0 and the B (with
-  // scales and zero points) of tile 1 and waits for tile 0.
+  // The ping-pong schedule (R(u) bar M(u) bar per tile, group 1 one barrier
+  // behind), with the DMA of tile u+2 (with its scales and zero points) inside
+  // M(u) -- between 32-cycle MFMAs a DMA issue does not stall the MFMA stream,
+  // and the read phase carries the dequant -- each wave waiting for its DMA at
+  // the end of its next read phase.
   if (nk > 0) {
-    static_for<5>([&](auto jc) { dma(0, jc); });
+    static_for<NDMA>([&](auto jc) { dma(0, jc); });
     if (wave == 0) dma_sz(0);
   }
   if (nk > 1) {
-    dma(1, std::integral_constant<int, 4>{});
+    static_for<NDMA>([&](auto jc) { dma(1, jc); });
     if (wave == 0) dma_sz(1);
-    wait_loads(std::integral_constant<int, 1>{}, std::integral_constant<int, NSZ>{});
-  } else {
-    wait_vmcnt<0>();
   }
+  wait_vmcnt<0>();
   bar();
   if (!g0) bar();
   int u = 0;
   for (; u + 2 < nk; ++u) {
-    read_phase(u, True{}, True{});
+    read_phase(u);
+    wait_vmcnt<0>();
     bar();
-    mfma_phase(True{});
+    mfma_phase(True{}, u + 2);
     bar();
   }
-  if (u + 1 < nk) {
-    read_phase(u, True{}, False{});
+  for (; u < nk; ++u) {
+    read_phase(u);
+    wait_vmcnt<0>();
     bar();
-    mfma_phase(False{});
-    bar();
-    ++u;
-  }
-  if (u < nk) {
-    read_phase(u, False{}, False{});
-    bar();
-    mfma_phase(False{});
+    mfma_phase(False{}, 0);
+    if (u + 1 < nk) bar();
   }
   if (g0) bar();
 
-  // ---- epilogue (as gemm_bf16_pingpong_kernel<., true>) ------------------------
+  // ---- epilogue --------------------------------------------------------------
   const bool partial_plane = p.split_k > 1;
   char* ybase = (char*)p.y + (partial_plane ? (size_t)part * p.y_split_stride : 0);
   const int row0 = m0 + g * 128;
   const int col0 = n0 + wn * TN;
   if (!partial_plane && p.out_bf16 && m0 + 256 <= (int)p.M && n0 + 256 <= (int)p.N && ((uintptr_t)p.y & 15) == 0) {
-    store_tile_bf16_staged16<FM>(p, acc, (char*)smem + wave * 16384, ybase, row0, col0, lane);
+    store_tile_bf16_staged<FM, FN>(p, acc, (char*)smem + wave * 16384, ybase, row0, col0, lane);
   } else {
     static_for<FM>([&](auto fmc) {
       constexpr int fm = decltype(fmc)::value;
-      const int m = row0 + fm * 16 + lr;
+      const int m = row0 + fm * 32 + lrow;
       if (m < (int)p.M) {
         static_for<FN>([&](auto fnc) {
           constexpr int fn = decltype(fnc)::value;
-          store_block16(p, acc[fn][fm], ybase, m, col0 + fn * 16 + lq * 4, partial_plane);
+          store_block(p, acc[fn][fm], ybase, m, col0 + fn * 32 + lhalf * 4, partial_plane);
         });
       }
     });
