@@ -546,13 +546,28 @@ def lds_patterns():
             ("x16_none", [(l % 16) * 128 + (l // 16) * 16 for l in range(64)]),
             ("x16_swz_lanes0-15_only", [(l % 16) * 128 + ((l // 16) ^ swz(l % 16)) * 16 if l < 16 else far(l)
                                         for l in range(64)]),
-            # rows of 32 K (64 bytes, 4 chunks; swizzle (r / 2 ^ (r >> 3) & 3) & 3), chunks 0-1 and 2-3
-            ("x32_k32_swz_c0", [(l % 32) * 64 + ((l // 32) ^ ((l % 32 // 2 ^ (l % 32 >> 3) & 3) & 3)) * 16
+            # rows of 32 K (64 bytes, 4 chunks), chunks 0-1 and 2-3: the former swizzle
+            # (r / 2 ^ (r >> 3) & 3) & 3, then the one the kernels use now, (r >> 2) & 3
+            ("x32_k32_old_c0", [(l % 32) * 64 + ((l // 32) ^ ((l % 32 // 2 ^ (l % 32 >> 3) & 3) & 3)) * 16
                                 for l in range(64)]),
-            ("x32_k32_swz_c2", [(l % 32) * 64 + ((2 + l // 32) ^ ((l % 32 // 2 ^ (l % 32 >> 3) & 3) & 3)) * 16
-                                for l in range(64)])]
+            ("x32_k32_old_c2", [(l % 32) * 64 + ((2 + l // 32) ^ ((l % 32 // 2 ^ (l % 32 >> 3) & 3) & 3)) * 16
+                                for l in range(64)]),
+            ("x32_k32_swz_c0", [(l % 32) * 64 + ((l // 32) ^ ((l % 32 >> 2) & 3)) * 16 for l in range(64)]),
+            ("x32_k32_swz_c2", [(l % 32) * 64 + ((2 + l // 32) ^ ((l % 32 >> 2) & 3)) * 16 for l in range(64)])]
+    x16 = lambda l: (l % 16) * 128 + ((l // 16) ^ swz(l % 16)) * 16
+    x32 = lambda l: (l % 32) * 128 + ((l // 32) ^ swz(l % 32)) * 16
+    pats += [("x16_swz_lanes16-31_only", [x16(l) if 16 <= l < 32 else far(l) for l in range(64)]),
+             ("x16_swz_lanes0-15_32-47_only", [x16(l) if (l & 31) < 16 else far(l) for l in range(64)]),
+             ("x32_swz_lanes0-31_only", [x32(l) if l < 32 else far(l) for l in range(64)]),
+             ("chunk_major_16_rows", [(l // 16) * 256 + (l % 16) * 16 for l in range(64)]),
+             ("lanes0-15_stride32", [32 * l if l < 16 else far(l) for l in range(64)]),
+             ("lanes0-31_interleaved_stride32", [32 * l if l < 16 else 32 * (l - 16) + 16 if l < 32 else far(l)
+                                                 for l in range(64)]),
+             ("lanes16-31_4096_apart", [16 * l if l < 16 else 16 * (l - 16) + 4096 if l < 32 else far(l)
+                                        for l in range(64)])]
     for b in range(6):
-        pats.append((f"bit{b}_same_bank", [(l & ~(1 << b)) * 16 + ((l >> b) & 1) * 1024 for l in range(64)]))
+        for d in ((1024,) if b in (1, 2) else (256, 512, 1024)):
+            pats.append((f"bit{b}_same_bank_{d}_apart", [(l & ~(1 << b)) * 16 + ((l >> b) & 1) * d for l in range(64)]))
     return pats
 
 

@@ -69,5 +69,6 @@ def test_probe_floors_print_one_json_line():
     r = run_bench("--only", "lds")
     assert r.returncode == 0, r.stderr[-2000:]
     out = json.loads(r.stdout.strip().splitlines()[-1])
-    assert [p["name"] for p in out["patterns"]][:3] == ["contiguous", "x32_swz", "x16_swz"]
+    names = [p["name"] for p in out["patterns"]]
+    assert names[:3] == ["contiguous", "x32_swz", "x16_swz"] and len(names) == 31
     assert all(p["us_per_launch"] > 0 for p in out["patterns"])
