@@ -35,7 +35,7 @@ def parse():
     p.add_argument("--steps", type=int, default=200)
     p.add_argument("--warmup", type=int, default=10)
     p.add_argument("--only", choices=["all", "gemm", "w4a16", "skinny", "prefill", "copy", "dispatch", "stream",
-                                      "mfma", "lds", "vendor"],
+                                      "mfma", "lds", "vendor", "persistent"],
                    default="all",
                    help="'copy' runs only a plain 1 GiB fp32 copy kernel: the calibration for rocprofv3 "
                         "FETCH_SIZE/WRITE_SIZE readings; 'dispatch' times batched submission (a batch of "
@@ -46,7 +46,8 @@ def parse():
                         "(32x32x16 / 16x16x32, operands in registers or re-read from LDS) with their shader "
                         "clocks; 'lds' one launch per LDS read pattern (for rocprofv3 bank-conflict counters); "
                         "'vendor' times torch.matmul (hipBLASLt) on the BASELINE GEMM shapes beside this "
-                        "library's kernels")
+                        "library's kernels; 'persistent' times the persistent decode preset beside the "
+                        "one-shot auto_select configuration")
     p.add_argument("--stream-bytes", type=int, default=0,
                    help="with --only stream: bytes per launch (default: the decode's 23,732,224); with "
                         "--stream-calibrate one non-temporal pass over this many bytes")
@@ -636,6 +637,49 @@ def bench_vendor(args, torch, t0mi):
                       "higher_is_better": False, "torch": torch.__version__, "results": res}), flush=True)
 
 
+def bench_persistent(args, torch, t0mi):
+    """The persistent preset tile_persistent_decode (tile_ir.rs:540-561) through t0mi_tile_gemm: one
+    launch of the persistent decode kernel, beside the one-shot configuration the cost model picks
+    for the same call (auto_select: split-K GEMM + reduce).  N(0,1) bf16 operands, f32 out; B is
+    rotated over copies totalling >= 512 MB so the Infinity Cache cannot serve repeats.  Bytes
+    per call: A, B and Y once."""
+    rt = t0mi.Runtime.on_torch_stream(0)
+    g = torch.Generator(device="cuda:0")
+    g.manual_seed(0x7901)
+    res = {}
+    cases = ((1, 4096, 4096, t0mi.NT), (16, 4096, 4096, t0mi.NT), (1, 4096, 4096, t0mi.NN),
+             (16, 4096, 4096, t0mi.NN), (32, 4096, 4096, t0mi.NT), (64, 4096, 4096, t0mi.NT),
+             (16, 11008, 4096, t0mi.NT))
+    preset = t0mi.tile_preset("tile_persistent_decode")
+    for m, n, k, tr in cases:
+        copies = max(2, -(-(512 << 20) // (2 * n * k)))
+        a = torch.randn(m, k, device="cuda:0", generator=g).to(torch.bfloat16)
+        shape_b = (k, n) if tr == t0mi.NN else (n, k)
+        bs = [torch.randn(*shape_b, device="cuda:0", generator=g).to(torch.bfloat16) for _ in range(copies)]
+        y = torch.empty(m, n, device="cuda:0", dtype=torch.float32)
+        spec = preset.copy(transpose=tr)
+        cfg = t0mi.auto_select_layout(m, k, n, tr, t0mi.OUT_F32).copy(transpose=tr, out_dtype=t0mi.OUT_F32)
+        pa, py = a.data_ptr(), y.data_ptr()
+        bp = [b.data_ptr() for b in bs]
+        alg = 2 * n * k + 2 * m * k + 4 * m * n
+        name = f"{m}x{n}x{k}_{'NN' if tr == t0mi.NN else 'NT'}"
+        row = {"bytes": alg}
+        for who, fn in (("persistent", lambda i: rt.tile_gemm(spec, pa, bp[i % copies], py, m, n, k)),
+                        ("one_shot:" + cfg.name(), lambda i: rt.gemm(cfg, pa, bp[i % copies], py, m, n, k))):
+            warm_up(torch, lambda fn=fn: fn(0), max(args.warmup, copies))
+            us, batches = timed_batches(torch, fn, max(args.steps, 2 * copies))
+            gbs = alg / (us * 1e-6) / 1e9
+            row[who] = {"us": round(us, 2), "GB/s": round(gbs, 1), "frac_hbm": round(gbs / PEAK_HBM_GBS, 4),
+                        "batch_us": [round(b, 2) for b in batches]}
+        res[name] = row
+        print(f"[bench] persistent {name}: " + ", ".join(f"{k_} {v['us']} us ({v['GB/s']} GB/s)"
+                                                       for k_, v in row.items() if k_ != "bytes"),
+              file=sys.stderr, flush=True)
+    rt.close()
+    print(json.dumps({"metric": "tile_persistent_decode vs the one-shot auto_select config, us per call",
+                      "unit": "us", "higher_is_better": False, "results": res}), flush=True)
+
+
 def bench_dispatch(args, torch, t0mi):
     """Host-visible cost per dispatch of a batch of small GEMMs (the prefill_dispatch.rs
     scenario: dozens of layers x a few kernels), three ways: a synchronous dispatch per
@@ -735,6 +779,9 @@ def main():
         return
     if args.only == "vendor":
         bench_vendor(args, torch, t0mi)
+        return
+    if args.only == "persistent":
+        bench_persistent(args, torch, t0mi)
         return
     rt = t0mi.Runtime.on_torch_stream(0)
     out = {"metric": METRIC, "n_gpus": 1, "steps": args.steps, "warmup": args.warmup, "higher_is_better": True,

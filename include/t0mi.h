@@ -358,15 +358,21 @@ int t0mi_tile_compute_grid(const t0mi_tile_spec* s, uint32_t m, uint32_t n, uint
  * three 16-K steps; NN tiles narrower than 64 columns on the 64-column NN
  * kernel).  The handle dispatches with the spec's own kernarg layout and grid;
  * M comes from the kernarg (0 = derive it from the grid, padded as gemm_gen
- * does).  A persistent spec (one workgroup looping over the N-tiles in the
- * reference, tile_ir.rs:540-561) runs as one launch of the configuration the
- * cost model picks for its (M, N, K), split-K included, with its epilogue.
- * T0MI_ERR_NO_KERNEL when no prebuilt kernel covers the tile. */
+ * does).  A persistent spec (one workgroup looping over the tiles in the
+ * reference, tile_ir.rs:540-604, 1062-1120) runs as one launch of a persistent
+ * kernel whose grid is what the GPU holds at once, each workgroup looping over
+ * work units with the grid's stride: up to 64 rows with K a multiple of 32 the
+ * decode kernel (32 x 16 units over the whole K, the K range split over the 16
+ * waves of a workgroup and summed in LDS in wave order), else the spec's tile
+ * kernel in a tile loop.  The whole K sum lands in Y (split-K is not part of a
+ * persistent run, as in the reference).  The kernarg's counter slot is left
+ * untouched.  T0MI_ERR_NO_KERNEL when no prebuilt kernel covers the tile. */
 int t0mi_tile_kernel_get(t0mi_ctx* ctx, const t0mi_tile_spec* s, t0mi_kernel** out);
 /* One-call tile GEMM: Y[m,n] = epilogue(X[m,k] . B) for the spec's transpose,
  * with the chain's arguments; split_k > 1 is reduced deterministically (the
  * reference's tile_ir split-K writes every partition to one plane,
- * tile_ir.rs:4577-4581; here the sum is correct).  Asynchronous. */
+ * tile_ir.rs:4577-4581; here the sum is correct).  A persistent spec takes the
+ * persistent kernels described at t0mi_tile_kernel_get.  Asynchronous. */
 int t0mi_tile_gemm(t0mi_ctx* ctx, const t0mi_tile_spec* s, uint64_t x, uint64_t wt, uint64_t y, uint32_t m,
                    uint32_t n, uint32_t k, uint64_t bias, float scale, float clamp_min, float clamp_max);
 

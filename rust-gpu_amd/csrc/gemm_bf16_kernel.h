@@ -141,15 +141,15 @@ __device__ __forceinline__ void store_block(const GemmParams& p, const f32x16& a
 
 // swz / swz_nn (the LDS swizzles) and the DMA chunk maps: index_maps.h.
 
-// Linear workgroup id -> (tile_m, tile_n, partition).
+// Linear work item `lin` of `nwg` -> (tile_m, tile_n, partition).
 // Workgroups are dispatched round-robin over the 8 XCDs; with xcd_remap the
-// ids that run on the same XCD (same L2) are made contiguous, then tiles are
+// items that run on the same XCD (same L2) are made contiguous, then tiles are
 // walked in groups of GROUP_M tile rows so each XCD works on a compact block
-// of output tiles (shared A rows / B columns stay L2-resident).
-__device__ __forceinline__ void tile_coords_of(uint32_t tiles_m, uint32_t tiles_n, uint32_t xcd_remap, int& tm,
-                                               int& tn, int& part) {
-  uint32_t nwg = gridDim.x * gridDim.y;
-  uint32_t lin = blockIdx.x + blockIdx.y * gridDim.x;
+// of output tiles (shared A rows / B columns stay L2-resident).  A persistent
+// kernel whose grid is a multiple of 8 keeps every item of a workgroup on that
+// workgroup's XCD, so the same numbering applies to its loop.
+__device__ __forceinline__ void tile_coords_lin(uint32_t lin, uint32_t nwg, uint32_t tiles_m, uint32_t tiles_n,
+                                                uint32_t xcd_remap, int& tm, int& tn, int& part) {
   if (xcd_remap && (nwg % 8u) == 0u) lin = (lin % 8u) * (nwg / 8u) + lin / 8u;
   uint32_t tiles = tiles_m * tiles_n;
   part = (int)(lin / tiles);
@@ -162,6 +162,13 @@ __device__ __forceinline__ void tile_coords_of(uint32_t tiles_m, uint32_t tiles_
   uint32_t r = t % group_size;
   tm = (int)(first_m + r % gm);
   tn = (int)(r / gm);
+}
+
+// The one-shot kernels: item = linear workgroup id.
+__device__ __forceinline__ void tile_coords_of(uint32_t tiles_m, uint32_t tiles_n, uint32_t xcd_remap, int& tm,
+                                               int& tn, int& part) {
+  tile_coords_lin(blockIdx.x + blockIdx.y * gridDim.x, gridDim.x * gridDim.y, tiles_m, tiles_n, xcd_remap, tm, tn,
+                  part);
 }
 
 __device__ __forceinline__ void tile_coords(const GemmParams& p, int& tm, int& tn, int& part) {
@@ -359,8 +366,10 @@ struct GemmTile {
   static_assert(!EVEN || LPT * (S - 1) <= 63, "vmcnt range");
 };
 
+// One output tile (tm, tn) of K partition `part`: the whole kernel body, called
+// once by gemm_bf16_kernel and in a loop by the persistent kernel.
 template <int BM, int BN, int BK, int WM, int WN, int S, bool NN>
-__global__ __launch_bounds__(WM * WN * 64) void gemm_bf16_kernel(GemmParams p) {
+__device__ __forceinline__ void gemm_bf16_tile(const GemmParams& p, int tm, int tn, int part) {
   using T = GemmTile<BM, BN, BK, WM, WN, S, NN>;
   constexpr int FM = T::FM, FN = T::FN, KC = T::KC, KS = T::KS, NC = T::NC;
   constexpr int TM = T::TM, TN = T::TN;
@@ -369,8 +378,6 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_bf16_kernel(GemmParams p) {
   constexpr int BUF = A_ELEMS + B_ELEMS;  // elements per LDS stage (A tile then B tile)
   __shared__ __attribute__((aligned(1024))) uint16_t smem[S * BUF];
 
-  int tm, tn, part;
-  tile_coords(p, tm, tn, part);
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
@@ -721,6 +728,13 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_bf16_kernel(GemmParams p) {
       });
     }
   });
+}
+
+template <int BM, int BN, int BK, int WM, int WN, int S, bool NN>
+__global__ __launch_bounds__(WM * WN * 64) void gemm_bf16_kernel(GemmParams p) {
+  int tm, tn, part;
+  tile_coords(p, tm, tn, part);
+  gemm_bf16_tile<BM, BN, BK, WM, WN, S, NN>(p, tm, tn, part);
 }
 
 }  // namespace t0mi

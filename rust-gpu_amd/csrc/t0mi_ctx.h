@@ -122,4 +122,23 @@ struct FixedWorkspace {
 int run_gemm(t0mi_ctx* ctx, const t0mi_gemm_config& cfg, const GemmLaunchEntry* e, uint64_t x, uint64_t b,
              uint64_t y, uint64_t bias, uint32_t m, uint32_t n, uint32_t k, const EpiChain& epi,
              const FixedWorkspace* fixed = nullptr);
+// True when the chain contains `op`.
+inline bool chain_uses(const EpiChain& e, uint32_t op) {
+  for (uint32_t i = 0; i < e.n; ++i)
+    if (((e.ops >> (4 * i)) & 0xFu) == op) return true;
+  return false;
+}
+// Persistent TileGemm specs (gemm_persistent.hip): up to this many rows (K a multiple
+// of 32, or 0) the decode kernel, else the spec's tile kernel with a grid-stride tile loop.
+constexpr uint32_t kPersistentDecodeRows = 64;
+// Which kernel a persistent run of `cfg` (the spec's lowered config) takes:
+// "decode", "tiles" (persistent tile loop) or "one-shot" (a tile with no persistent
+// instantiation: the one-shot kernel of the same tile).
+const char* persistent_route(const t0mi_gemm_config& cfg, uint32_t m, uint32_t n, uint32_t k);
+// Y = epi(X . B) for a persistent spec: one launch of a persistent kernel, the whole K
+// sum in one plane (as the reference's persistent lowering, which ignores split-K).
+// Asynchronous.
+int run_gemm_persistent(t0mi_ctx* ctx, const t0mi_gemm_config& cfg, const GemmLaunchEntry* e, uint64_t x,
+                        uint64_t b, uint64_t y, uint64_t bias, uint32_t m, uint32_t n, uint32_t k,
+                        const EpiChain& epi);
 }  // namespace t0mi

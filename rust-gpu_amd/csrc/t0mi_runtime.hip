@@ -250,11 +250,6 @@ EpiChain chain_of(uint32_t gemm_gen_epilogue) {
   return e;
 }
 
-static bool chain_uses(const EpiChain& e, uint32_t op) {
-  for (uint32_t i = 0; i < e.n; ++i)
-    if (((e.ops >> (4 * i)) & 0xFu) == op) return true;
-  return false;
-}
 
 int launch_splitk_reduce(t0mi_ctx* ctx, const float* ws, void* y, const float* bias, uint32_t M, uint32_t N,
                          uint32_t ldy, uint32_t sk, uint32_t out_bf16, const EpiChain& epilogue) {
@@ -609,13 +604,14 @@ static int dispatch_tile(t0mi_ctx* ctx, const t0mi_kernel* k, const uint32_t gri
     chain.lo = rd_f32(ka + k->lay.clamp_min);
     chain.hi = rd_f32(ka + k->lay.clamp_max);
   }
-  if (s.persistent && (sk == 1 || yss == 0))
-    // tile_ir.rs:540-561: one workgroup loops over every N-tile so that a
-    // decode-sized GEMM pays one dispatch (an RDNA scheduling workaround).  On
-    // gfx950 one workgroup is one of 256 CUs, so the spec runs as one launch of
-    // the configuration the cost model picks for (M, N, K) — split-K when the
-    // tiles alone would leave CUs idle — with the spec's epilogue.
-    return run_gemm_auto(ctx, s.transpose, x, wt, y, M, N, K, T0MI_OUT_F32, bias, &chain);
+  if (s.persistent)
+    // tile_ir.rs:540-604, 1062-1120: one workgroup loops over every tile so that a
+    // decode-sized GEMM is one dispatch; split-K is not part of a persistent run
+    // (split_k_id = 0), so the whole sum lands in Y.  Here: one launch of a
+    // persistent kernel whose grid is what the GPU holds at once.  The kernarg's
+    // counter, n_tiles_n_shift and tiles_per_wg describe the reference's
+    // one-workgroup schedule; the grid-stride schedule derives its own from M, N.
+    return run_gemm_persistent(ctx, k->cfg, k->gemm, x, wt, y, bias, M, N, K, chain);
   if (sk == 1 || yss == 0)
     // One output plane: split-K partitions are summed by the library.
     return run_gemm(ctx, k->cfg, k->gemm, x, wt, y, bias, M, N, K, chain);
@@ -901,5 +897,6 @@ extern "C" int t0mi_tile_gemm(t0mi_ctx* ctx, const t0mi_tile_spec* s, uint64_t x
   chain.scale = scale;
   chain.lo = clamp_min;
   chain.hi = clamp_max;
+  if (s->persistent) return run_gemm_persistent(ctx, cfg, e, x, wt, y, bias, m, n, k, chain);
   return run_gemm(ctx, cfg, e, x, wt, y, bias, m, n, k, chain);
 }
