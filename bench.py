@@ -294,6 +294,37 @@ def w4a16_graph_us(torch, t0mi, pa, wp, py, Mw, Kw, Nw, G, copies):
         rt2.close()
 
 
+def graph_replay_us(torch, t0mi, call, n):
+    """Per-call time of n calls call(rt, i) captured into a HIP graph on a fresh runtime's
+    stream and replayed (no host enqueue cost); call(rt, 0) runs once first so the runtime's
+    buffers exist before the capture.  Median over BATCHES replays."""
+    rt2 = t0mi.Runtime(device=0)
+    try:
+        ext = torch.cuda.ExternalStream(rt2.stream)
+        torch.cuda.synchronize()
+        call(rt2, 0)
+        t0mi.check(rt2.wait_idle())
+        rt2.capture_begin()
+        for i in range(n):
+            call(rt2, i)
+        graph = rt2.capture_end()
+        vals = []
+        for rep in range(3 + BATCHES):
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record(ext)
+            graph.launch()
+            e1.record(ext)
+            t0mi.check(rt2.wait_idle())
+            e1.synchronize()
+            if rep >= 3:
+                vals.append(e0.elapsed_time(e1) * 1e3 / n)
+        graph.destroy()
+        vals.sort()
+        return round(vals[len(vals) // 2], 3)
+    finally:
+        rt2.close()
+
+
 def cpu_model() -> str:
     """The host CPU's model name (from /proc/cpuinfo) and its logical CPU count."""
     name = "unknown"
@@ -664,15 +695,21 @@ def bench_persistent(args, torch, t0mi):
         alg = 2 * n * k + 2 * m * k + 4 * m * n
         name = f"{m}x{n}x{k}_{'NN' if tr == t0mi.NN else 'NT'}"
         row = {"bytes": alg}
-        for who, fn in (("persistent", lambda i: rt.tile_gemm(spec, pa, bp[i % copies], py, m, n, k)),
-                        ("one_shot:" + cfg.name(), lambda i: rt.gemm(cfg, pa, bp[i % copies], py, m, n, k))):
+        for who, fn, gcall in (
+                ("persistent", lambda i: rt.tile_gemm(spec, pa, bp[i % copies], py, m, n, k),
+                 lambda r, i: r.tile_gemm(spec, pa, bp[i % copies], py, m, n, k)),
+                ("one_shot:" + cfg.name(), lambda i: rt.gemm(cfg, pa, bp[i % copies], py, m, n, k),
+                 lambda r, i: r.gemm(cfg, pa, bp[i % copies], py, m, n, k))):
             warm_up(torch, lambda fn=fn: fn(0), max(args.warmup, copies))
             us, batches = timed_batches(torch, fn, max(args.steps, 2 * copies))
             gbs = alg / (us * 1e-6) / 1e9
+            gus = graph_replay_us(torch, t0mi, gcall, 4 * copies)
             row[who] = {"us": round(us, 2), "GB/s": round(gbs, 1), "frac_hbm": round(gbs / PEAK_HBM_GBS, 4),
-                        "batch_us": [round(b, 2) for b in batches]}
+                        "batch_us": [round(b, 2) for b in batches], "graph_replay_us": gus,
+                        "graph_GB/s": round(alg / (gus * 1e-6) / 1e9, 1)}
         res[name] = row
-        print(f"[bench] persistent {name}: " + ", ".join(f"{k_} {v['us']} us ({v['GB/s']} GB/s)"
+        print(f"[bench] persistent {name}: " + ", ".join(f"{k_} {v['us']} us ({v['GB/s']} GB/s; graph "
+                                                       f"{v['graph_replay_us']} us)"
                                                        for k_, v in row.items() if k_ != "bytes"),
               file=sys.stderr, flush=True)
     rt.close()
