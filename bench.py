@@ -35,7 +35,7 @@ def parse():
     p.add_argument("--steps", type=int, default=200)
     p.add_argument("--warmup", type=int, default=10)
     p.add_argument("--only", choices=["all", "gemm", "w4a16", "skinny", "prefill", "copy", "dispatch", "stream",
-                                      "mfma", "lds", "vendor", "persistent"],
+                                      "mfma", "lds", "vendor", "persistent", "picks"],
                    default="all",
                    help="'copy' runs only a plain 1 GiB fp32 copy kernel: the calibration for rocprofv3 "
                         "FETCH_SIZE/WRITE_SIZE readings; 'dispatch' times batched submission (a batch of "
@@ -47,7 +47,8 @@ def parse():
                         "clocks; 'lds' one launch per LDS read pattern (for rocprofv3 bank-conflict counters); "
                         "'vendor' times torch.matmul (hipBLASLt) on the BASELINE GEMM shapes beside this "
                         "library's kernels; 'persistent' times the persistent decode preset beside the "
-                        "one-shot auto_select configuration")
+                        "one-shot auto_select configuration; 'picks' times auto_select's pick against the "
+                        "cost model's other top candidates on a set of shapes")
     p.add_argument("--stream-bytes", type=int, default=0,
                    help="with --only stream: bytes per launch (default: the decode's 23,732,224); with "
                         "--stream-calibrate one non-temporal pass over this many bytes")
@@ -717,6 +718,52 @@ def bench_persistent(args, torch, t0mi):
                       "unit": "us", "higher_is_better": False, "results": res}), flush=True)
 
 
+PICK_SHAPES = ((1, 4096, 4096), (16, 4096, 4096), (64, 4096, 4096), (128, 4096, 4096), (256, 4096, 4096),
+               (16, 11008, 4096), (32, 11008, 4096), (512, 11008, 4096), (512, 512, 512), (1024, 1024, 1024),
+               (2048, 2048, 2048), (1024, 4096, 4096))
+
+
+def bench_picks(args, torch, t0mi):
+    """auto_select's pick (the head of cost_model::auto_schedule_gemm, cost_model.rs:464-534) against
+    the model's next candidates, per shape: NN, bf16 out, N(0,1) bf16, B rotated over >= 256 MB,
+    median of 3 event-timed batches; 4- and 5-stage copies of a 3-stage tile are skipped."""
+    rt = t0mi.Runtime.on_torch_stream(0)
+    g = torch.Generator(device="cuda:0")
+    g.manual_seed(3)
+    res = []
+    for (m, n, k) in PICK_SHAPES:
+        ranked = t0mi.auto_schedule_gemm(m, n, k, t0mi.NN, t0mi.OUT_BF16, cap=64)
+        cands, seen = [], set()
+        for c, e in ranked:
+            key = (c.tile_m, c.tile_n, c.tile_k, c.wave_m, c.wave_n, c.split_k)
+            if c.stages in (4, 5) and key in seen:
+                continue
+            seen.add(key)
+            cands.append((c, e))
+            if len(cands) == 10:
+                break
+        copies = max(2, -(-(256 << 20) // (2 * n * k)))
+        a = torch.randn(m, k, device="cuda:0", generator=g).to(torch.bfloat16)
+        bs = [torch.randn(k, n, device="cuda:0", generator=g).to(torch.bfloat16) for _ in range(copies)]
+        y = torch.empty(m, n, device="cuda:0", dtype=torch.bfloat16)
+        rows = []
+        for c, e in cands:
+            f = lambda i, c=c: rt.gemm(c, a.data_ptr(), bs[i % copies].data_ptr(), y.data_ptr(), m, n, k)
+            warm_up(torch, lambda: f(0), 4, min_s=0.05)
+            us, _ = timed_batches(torch, f, max(60, 2 * copies), batches=3)
+            rows.append({"config": c.name(), "est_us": round(e, 2), "us": round(us, 2)})
+        best = min(rows, key=lambda r: r["us"])
+        res.append({"shape": [m, n, k], "pick": rows[0], "best": best,
+                    "pick_over_best": round(rows[0]["us"] / best["us"], 3), "candidates": rows})
+        print(f"[bench] picks {m}x{n}x{k}: pick {rows[0]['config']} {rows[0]['us']} us, best {best['config']} "
+              f"{best['us']} us", file=sys.stderr, flush=True)
+        del a, bs, y
+    rt.close()
+    mean = sum(r["pick_over_best"] for r in res) / len(res)
+    print(json.dumps({"metric": "auto_select pick / fastest of the cost model's top candidates", "unit": "ratio",
+                      "higher_is_better": False, "value": round(mean, 4), "results": res}), flush=True)
+
+
 def bench_dispatch(args, torch, t0mi):
     """Host-visible cost per dispatch of a batch of small GEMMs (the prefill_dispatch.rs
     scenario: dozens of layers x a few kernels), three ways: a synchronous dispatch per
@@ -819,6 +866,9 @@ def main():
         return
     if args.only == "persistent":
         bench_persistent(args, torch, t0mi)
+        return
+    if args.only == "picks":
+        bench_picks(args, torch, t0mi)
         return
     rt = t0mi.Runtime.on_torch_stream(0)
     out = {"metric": METRIC, "n_gpus": 1, "steps": args.steps, "warmup": args.warmup, "higher_is_better": True,

@@ -135,6 +135,12 @@ int t0mi_build_kernargs_with_bias(uint64_t x, uint64_t wt, uint64_t y, uint32_t 
  * cost model over the prebuilt kernels.  transpose / out_dtype of the result
  * are T0MI_NT / T0MI_OUT_F32 like the reference; callers set them after. */
 int t0mi_auto_select(uint32_t m, uint32_t k, uint32_t n, t0mi_gemm_config* out);
+/* cost_model::auto_schedule_gemm (src/t0/cost_model.rs:464-534; note its
+ * (m, n, k) order): the ranking behind t0mi_auto_select_layout -- every
+ * prebuilt configuration of the layout, best first, with the model's estimate
+ * in microseconds.  Writes up to cap entries; *count = the full list length. */
+int t0mi_auto_schedule_gemm(uint32_t m, uint32_t n, uint32_t k, uint32_t transpose, uint32_t out_dtype,
+                            t0mi_gemm_config* out, double* est_us, uint32_t cap, uint32_t* count);
 /* auto_select_legacy (gemm_gen.rs:351-404), re-derived for gfx950. */
 int t0mi_auto_select_legacy(uint32_t m, uint32_t k, uint32_t n, t0mi_gemm_config* out);
 /* gfx950 extension of auto_select (gemm_gen.rs:340), which only knows the NT

@@ -260,13 +260,27 @@ static double estimate_us(const t0mi_gemm_config& c, uint32_t m, uint32_t n, uin
   const double hide = W * wg_per_cu / 4.0 < 2.0 ? 0.8 : 1.0;
   const double t_comp = rounds * wg_per_cu * flops_tile / (FLOP_PER_CLK_CU * CLK * eff * busy * hide);
   const double out_b = c.out_dtype == T0MI_OUT_BF16 ? 2.0 : 4.0;
-  double hbm_bytes = 2.0 * m * k + 2.0 * k * n + (sk > 1 ? sk * 4.0 : out_b) * m * n;
+  double hbm_bytes = 2.0 * m * k + 2.0 * k * n + (sk > 1 ? 0.0 : out_b) * m * n;
   const double l2_bytes = tiles * (c.tile_m + c.tile_n) * kp * 2.0;
-  const double t_mem = std::max(hbm_bytes / HBM, l2_bytes / L2);
+  // A CU streams its workgroups' tiles (and split-K planes) at ~55 GB/s through
+  // the LDS DMA of these kernels (measured: 128 x 4096 x 4096 with 128 x 128
+  // tiles, split-K 8 on 256 CUs streams 256 KB per CU in ~5 us; split-K 4 on
+  // 128 CUs, twice the bytes per CU, is ~2.4 us slower), so a grid that leaves
+  // CUs idle cannot reach the HBM rate.
+  const double R_CU = 55.0e9;
+  const double cu_bytes =
+      rounds * wg_per_cu * ((c.tile_m + c.tile_n) * kp * 2.0 + (sk > 1 ? c.tile_m * c.tile_n * 4.0 : 0.0));
+  const double t_mem = std::max({hbm_bytes / HBM, l2_bytes / L2, cu_bytes / R_CU});
   double t = std::max(t_comp, t_mem) * 1e6 + 3.0;
   // The split-K reduce pass is a separate launch: it reads every fp32 partial
-  // plane and writes the output once.
-  if (sk > 1) t += (sk * 4.0 + out_b) * m * n / HBM * 1e6 + 3.0;
+  // plane, just written and mostly served by the Infinity Cache (~12 TB/s:
+  // 16.8 MB in 4.2 us with its launch), and writes the output once.
+  if (sk > 1) t += (sk * 4.0 * m * n / 12.0e12 + out_b * m * n / HBM) * 1e6 + 3.0;
+  // The split-K planes are stored after the K loops, all workgroups at once, so
+  // their write does not overlap the streaming of the operands (1024 x 4096 x
+  // 4096 with 256 x 256 tiles at split-K 4 writes 64 MB of planes: 47.8 us,
+  // against 43.3 us unsplit with 128 x 128 tiles).
+  if (sk > 1) t += sk * 4.0 * m * n / HBM * 1e6;
   return t;
 }
 
@@ -303,8 +317,10 @@ std::vector<t0mi_gemm_config> rank_candidates(uint32_t m, uint32_t n, uint32_t k
   for (const auto& v : gemm_variants()) {
     if (v.nn != want_nn) continue;
     for (uint32_t sk = 1; sk <= 16; sk *= 2) {
-      // Each partition keeps at least two K tiles.
-      if (sk > 1 && (uint64_t)k < (uint64_t)sk * v.bk * 2) break;
+      // Each partition keeps at least eight K tiles: with fewer, the per-workgroup
+      // prologue, plane store and the reduce launch outweigh the shorter K loop
+      // (1024^3 with 128 x 128 tiles: 12.5 us unsplit, 18.2 us at split-K 4).
+      if (sk > 1 && (uint64_t)k < (uint64_t)sk * v.bk * 8) break;
       t0mi_gemm_config c = make_cfg(v.bm, v.bn, v.bk, v.wm, v.wn, sk, transpose, out_dtype, v.stages);
       if (!config_feasible(c, nullptr)) continue;
       scored.push_back({estimate_us(c, m, n, k), c});
@@ -521,6 +537,23 @@ extern "C" int t0mi_auto_select_layout(uint32_t m, uint32_t k, uint32_t n, uint3
   auto c = rank_candidates(m, n, k, transpose, out_dtype, nullptr);
   if (c.empty()) return set_error(T0MI_ERR_NO_KERNEL, "no prebuilt kernel for %ux%ux%u", m, n, k);
   *out = c[0];
+  return T0MI_OK;
+}
+
+extern "C" int t0mi_auto_schedule_gemm(uint32_t m, uint32_t n, uint32_t k, uint32_t transpose, uint32_t out_dtype,
+                                       t0mi_gemm_config* out, double* est_us, uint32_t cap, uint32_t* count) {
+  // cost_model::auto_schedule_gemm (src/t0/cost_model.rs:464-534): every feasible
+  // prebuilt configuration of the layout, best first, with its estimate.
+  if (!count || (cap && !out)) return set_error(T0MI_ERR_INVALID, "null output");
+  if (!m || !n || !k) return set_error(T0MI_ERR_INVALID, "zero dimension");
+  if (transpose > T0MI_NN || out_dtype > T0MI_OUT_BF16) return set_error(T0MI_ERR_INVALID, "bad layout or out_dtype");
+  std::vector<double> est;
+  auto c = rank_candidates(m, n, k, transpose, out_dtype, &est);
+  *count = (uint32_t)c.size();
+  for (uint32_t i = 0; i < cap && i < c.size(); ++i) {
+    out[i] = c[i];
+    if (est_us) est_us[i] = est[i];
+  }
   return T0MI_OK;
 }
 

@@ -161,6 +161,7 @@ SIGNATURES = {
     "t0mi_auto_select": (_I, [_U32, _U32, _U32, _CFG]),
     "t0mi_auto_select_legacy": (_I, [_U32, _U32, _U32, _CFG]),
     "t0mi_auto_select_layout": (_I, [_U32, _U32, _U32, _U32, _U32, _CFG]),
+    "t0mi_auto_schedule_gemm": (_I, [_U32, _U32, _U32, _U32, _U32, _P, _P, _U32, ctypes.POINTER(_U32)]),
     "t0mi_cached_auto_select": (_I, [_U32, _U32, _U32, _CFG]),
     "t0mi_clear_spec_cache": (None, []),
     "t0mi_spec_cache_len": (_SZ, []),
@@ -361,6 +362,17 @@ def auto_select_layout(m: int, k: int, n: int, transpose: int = NN, out_dtype: i
     c = GemmConfig()
     check(lib().t0mi_auto_select_layout(m, k, n, transpose, out_dtype, ctypes.byref(c)))
     return c
+
+
+def auto_schedule_gemm(m: int, n: int, k: int, transpose: int = NN, out_dtype: int = OUT_F32, cap: int = 64):
+    """cost_model::auto_schedule_gemm (src/t0/cost_model.rs:464-534): [(GemmConfig, estimated us)],
+    best first, at most cap entries (note the reference's (m, n, k) order)."""
+    cfgs = (GemmConfig * cap)()
+    est = (ctypes.c_double * cap)()
+    count = ctypes.c_uint32(0)
+    check(lib().t0mi_auto_schedule_gemm(m, n, k, transpose, out_dtype, ctypes.cast(cfgs, _P), ctypes.cast(est, _P),
+                                        cap, ctypes.byref(count)))
+    return [(cfgs[i].copy(), est[i]) for i in range(min(cap, count.value))]
 
 
 def auto_select_legacy(m: int, k: int, n: int) -> GemmConfig:

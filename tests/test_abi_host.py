@@ -128,6 +128,27 @@ def test_auto_select_domain_sample_feasible_and_prebuilt():
     assert (big.tile_m, big.tile_n) == (256, 256), big.name()
 
 
+def test_auto_schedule_gemm_ranking():
+    """cost_model.rs:464-534: feasible configs best first; the head is auto_select's pick for the
+    layout; every entry has a prebuilt kernel; cap bounds what is written, not the count."""
+    for (m, n, k) in ((128, 4096, 4096), (4096, 4096, 4096), (16, 11008, 4096), (100, 200, 64)):
+        for tr in (t0mi.NT, t0mi.NN):
+            ranked = t0mi.auto_schedule_gemm(m, n, k, tr, t0mi.OUT_BF16, cap=256)
+            assert ranked, (m, n, k, tr)
+            est = [e for _, e in ranked]
+            assert est == sorted(est) and all(e > 0 for e in est)
+            pick = t0mi.auto_select_layout(m, k, n, tr, t0mi.OUT_BF16)
+            assert ranked[0][0].name() == pick.name()
+            rt = t0mi.Runtime(null=True)
+            for c, _ in ranked:
+                assert c.is_feasible() and c.transpose == tr
+                rt.kernel(c)
+            short = t0mi.auto_schedule_gemm(m, n, k, tr, t0mi.OUT_BF16, cap=3)
+            assert [c.name() for c, _ in short] == [c.name() for c, _ in ranked[:3]]
+    with pytest.raises(t0mi.T0miError):
+        t0mi.auto_schedule_gemm(0, 64, 64)
+
+
 def test_auto_select_legacy():
     """gemm_gen.rs:636-646: small squares use split-K with tile_m 64; 1024^3 uses tile_m 128."""
     c = t0mi.auto_select_legacy(256, 256, 256)
