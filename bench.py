@@ -720,7 +720,8 @@ def bench_persistent(args, torch, t0mi):
 
 PICK_SHAPES = ((1, 4096, 4096), (16, 4096, 4096), (64, 4096, 4096), (128, 4096, 4096), (256, 4096, 4096),
                (16, 11008, 4096), (32, 11008, 4096), (512, 11008, 4096), (512, 512, 512), (1024, 1024, 1024),
-               (2048, 2048, 2048), (1024, 4096, 4096))
+               (2048, 2048, 2048), (1024, 4096, 4096), (768, 11008, 4096), (1536, 11008, 4096),
+               (2048, 11008, 4096), (1536, 14336, 4096))
 
 
 def bench_picks(args, torch, t0mi):

@@ -258,7 +258,14 @@ static double estimate_us(const t0mi_gemm_config& c, uint32_t m, uint32_t n, uin
   // reads and barriers (measured: 256x256 with 4 waves runs ~10% slower than
   // with 8 at 4096^3, despite the larger per-wave MFMA blocks).
   const double hide = W * wg_per_cu / 4.0 < 2.0 ? 0.8 : 1.0;
-  const double t_comp = rounds * wg_per_cu * flops_tile / (FLOP_PER_CLK_CU * CLK * eff * busy * hide);
+  // A last, partly filled round of tiles runs on a lightly loaded GPU (the power
+  // limit no longer sets the clock): 0.6 of a full round when nearly empty
+  // (1536 x 11008 x 4096 with 256 x 256 tiles, 258 tiles on 256 CUs: 158 us,
+  // against ~94 us per full round at 4096^3).
+  const double slots = CUS * wg_per_cu;
+  const double full_rounds = floor(tiles / slots), rest = tiles - full_rounds * slots;
+  const double rounds_c = full_rounds + (rest > 0 ? 0.6 + 0.4 * rest / slots : 0.0);
+  const double t_comp = rounds_c * wg_per_cu * flops_tile / (FLOP_PER_CLK_CU * CLK * eff * busy * hide);
   const double out_b = c.out_dtype == T0MI_OUT_BF16 ? 2.0 : 4.0;
   double hbm_bytes = 2.0 * m * k + 2.0 * k * n + (sk > 1 ? 0.0 : out_b) * m * n;
   const double l2_bytes = tiles * (c.tile_m + c.tile_n) * kp * 2.0;
