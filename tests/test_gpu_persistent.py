@@ -180,3 +180,27 @@ def test_persistent_dispatch_kernarg(rt):
     assert np.array_equal(y, reference(spec, a, b, bias, False))
     # the counter is the reference's bookkeeping slot: the gfx950 schedule leaves it untouched
     assert not from_dev(dcnt, np.uint8, (4096,)).any()
+
+
+def _random_persistent_cases(n_cases=24, seed=0x9E75):
+    """Seeded ragged shapes for the three persistent presets: rows 1..300 (both kernels), N and
+    K multiples of 8 (K not always a multiple of 32, so the decode rows take the tile loop)."""
+    g = np.random.default_rng(seed)
+    presets = ["tile_persistent_decode", "tile_persistent_128x64_k32", "tile_persistent_256x128_k32"]
+    out = []
+    for i in range(n_cases):
+        m = int(g.choice([int(g.integers(1, 65)), int(g.integers(65, 300))]))
+        n = 8 * int(g.integers(1, 200))
+        k = 8 * int(g.integers(0, 160))
+        out.append((i, presets[i % 3], m, n, k, int(g.integers(0, 2))))
+    return out
+
+
+@pytest.mark.parametrize("i,preset,m,n,k,nn", _random_persistent_cases())
+def test_random_shapes_integer_exact(rt, i, preset, m, n, k, nn):
+    # integer inputs: every route (decode kernel, tile loop) must give the oracle's exact values
+    spec = spec_of(preset, nn)
+    a, b = int_pattern(m, k, n, nn, seed=i)
+    bias = ((np.arange(n) % 9) - 4).astype(np.float32)
+    y = run(rt, spec, a, b, m, n, k, bias)
+    assert np.array_equal(y, reference(spec, a, b, bias, nn))
