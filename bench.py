@@ -212,13 +212,20 @@ def bench_prefill(args, torch, t0mi, rt):
 
     def launch(i=0):
         rt.w4a16_gemm(*args_)
-    warm_up(torch, launch, args.warmup)
-    us, batches = timed_batches(torch, launch, args.steps)
-    tflops = 2.0 * M * N * K / (us * 1e-6) / 1e12
-    print(f"[bench] prefill w4a16 4096x4096x14336 g128 zeros: {us:.1f} us/call (median of "
-          f"{', '.join(f'{b:.1f}' for b in batches)}), {tflops:.1f} TFLOPS "
-          f"({100*tflops/PEAK_BF16_TFLOPS:.1f}% of peak)", file=sys.stderr, flush=True)
-    return us, tflops
+    res = {}
+    # The default route, then the fused route a caller gets with a zero workspace limit
+    # (dequant inside the K loop, no bf16 weight buffer).
+    for route, limit in (("default", 2**64 - 1), ("fused", 0)):
+        rt.set_w4a16_workspace_limit(limit)
+        warm_up(torch, launch, args.warmup)
+        us, batches = timed_batches(torch, launch, args.steps)
+        tflops = 2.0 * M * N * K / (us * 1e-6) / 1e12
+        res[route] = (us, tflops)
+        print(f"[bench] prefill w4a16 4096x4096x14336 g128 zeros, {route} route: {us:.1f} us/call (median of "
+              f"{', '.join(f'{b:.1f}' for b in batches)}), {tflops:.1f} TFLOPS "
+              f"({100*tflops/PEAK_BF16_TFLOPS:.1f}% of peak)", file=sys.stderr, flush=True)
+    rt.set_w4a16_workspace_limit(2**64 - 1)
+    return res["default"][0], res["default"][1], res["fused"]
 
 
 def bench_w4a16(args, torch, t0mi, rt):
@@ -889,8 +896,12 @@ def main():
         print(json.dumps(out), flush=True)
         return
     if args.only == "prefill":
-        us, tflops = bench_prefill(args, torch, t0mi, rt)
+        us, tflops, (fus_us, fus_tf) = bench_prefill(args, torch, t0mi, rt)
         out.update({"metric": "W4A16 prefill TFLOPS (% MFMA peak)", "value": round(tflops, 2), "unit": "TFLOPS",
+                    "fused_route": {"us": round(fus_us, 2), "TFLOPS": round(fus_tf, 2),
+                                    "frac": round(fus_tf / PEAK_BF16_TFLOPS, 4),
+                                    "how": "t0mi_set_w4a16_workspace_limit(ctx, 0): dequant inside the K loop",
+                                    "traffic": (load_traffic("w4a16_prefill_fused_detail") or {}).get("call_bytes")},
                     "ms_per_step": round(us * 1e-3, 6),
                     "config": {"workload": "W4A16 A[4096,4096] bf16 x int4 W[4096,14336] g128, per-group zero "
                                            "points, bf16 out (BASELINE config 5); one call = t0mi_w4a16_gemm"},

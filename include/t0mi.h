@@ -434,11 +434,23 @@ int t0mi_auto_gemm(t0mi_ctx* ctx, uint64_t a, uint64_t b, uint64_t c, uint32_t m
  * CUs; from 1536 rows (768 when K or the group is not a multiple of 64, and
  * from 81 rows for a group that is not a power of two) the weight is
  * dequantized once to bf16 into the library's conversion buffer (k * n * 2
- * bytes, kept by the runtime) and the dense NN GEMM runs.  The ping-pong and
- * the dequant-once routes give bit-identical results on the same problem. */
+ * bytes, kept by the runtime) and the dense NN GEMM runs, unless that is above
+ * the runtime's limit (t0mi_set_w4a16_workspace_limit).  The ping-pong and the
+ * dequant-once routes give bit-identical results when the dense GEMM takes the
+ * same 256x256 tile and K partitions (4096 rows and more: config 5). */
 int t0mi_w4a16_gemm(t0mi_ctx* ctx, uint64_t a, uint64_t qweight, uint64_t scales, uint64_t qzeros,
                     uint32_t zp_const, uint64_t y, uint32_t m, uint32_t k, uint32_t n, uint32_t group,
                     uint32_t out_dtype);
+/* No counterpart in the reference (which has no fused W4A16 GEMM).  For callers
+ * that cannot hold the dequantized weight (k * n * 2 bytes of the runtime's
+ * conversion buffer): t0mi_w4a16_gemm calls on this runtime whose dequant-once
+ * route would need more than `bytes` run the fused kernels instead -- the
+ * 256x256 ping-pong kernel (K and group multiples of 64) or the 128x128 fused
+ * tile kernel (other power-of-two groups), the weights crossing HBM once, at 4
+ * bits; with a group that is neither, such calls return T0MI_ERR_INVALID.
+ * Results are those of the default route (the ping-pong kernel's are
+ * bit-identical to dequant-once).  Default: no limit.  0: never dequantize once. */
+int t0mi_set_w4a16_workspace_limit(t0mi_ctx* ctx, uint64_t bytes);
 
 /* Standalone dequant, replacing build_dequant_int4_{f32,bf16} (quant_kernels.rs:53-171)
  * on the same layouts as t0mi_w4a16_gemm: out[k][n] = (float)(q - z) * s.

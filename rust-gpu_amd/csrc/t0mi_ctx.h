@@ -67,6 +67,9 @@ struct t0mi_ctx {
   // from ws, which the GEMMs they launch may use for split-K).
   void* cvt = nullptr;
   size_t cvt_bytes = 0;
+  // Largest dequantized-weight buffer (bytes) t0mi_w4a16_gemm may use for its
+  // dequant-once route; above it the fused kernels run instead.
+  uint64_t w4_cvt_limit = ~0ull;
   // This device's copy of the library's static scratch array (device
   // address, looked up once per device when the first runtime on it is
   // created) and the error of that lookup if it failed.  Used only by

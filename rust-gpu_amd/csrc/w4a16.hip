@@ -423,6 +423,14 @@ static int launch_w4_pingpong(t0mi_ctx* ctx, uint64_t a, uint64_t qweight, uint6
   return T0MI_OK;
 }
 
+extern "C" int t0mi_set_w4a16_workspace_limit(t0mi_ctx* ctx, uint64_t bytes) {
+  int rc = check_ctx(ctx);
+  if (rc) return rc;
+  T0MI_SUBMIT_GUARD(ctx);
+  ctx->w4_cvt_limit = bytes;
+  return T0MI_OK;
+}
+
 extern "C" int t0mi_w4a16_gemm(t0mi_ctx* ctx, uint64_t a, uint64_t qweight, uint64_t scales, uint64_t qzeros,
                                uint32_t zp_const, uint64_t y, uint32_t m, uint32_t k, uint32_t n, uint32_t group,
                                uint32_t out_dtype) {
@@ -462,9 +470,19 @@ extern "C" int t0mi_w4a16_gemm(t0mi_ctx* ctx, uint64_t a, uint64_t qweight, uint
   const bool v2_group = group == 32 || group == 64 || group == 128 || group == 256;
   const uint32_t decode_max = v2_group ? 16 * decode_max_slabs(group) * kDecodeMaxLaunches : kDecodeMaxRows;
   const bool pingpong = w4_pingpong_ok(k, group, 1, k);
-  if (pingpong && m >= kPingPongRows && m < kTwoPassRows)
+  bool two_pass = m >= (pingpong ? kTwoPassRows : kPrefillTwoPassRows) || (m > decode_max && !pow2_group);
+  if (two_pass && (uint64_t)k * n * 2 > ctx->w4_cvt_limit) {
+    // The caller's limit on the conversion buffer: dequantize inside the K loop instead.
+    if (!pingpong && !pow2_group)
+      return set_error(T0MI_ERR_INVALID,
+                       "%u rows with group %u need the %llu-byte dequantized weight buffer, above the limit "
+                       "of %llu bytes (no fused kernel takes this group)",
+                       m, group, (unsigned long long)k * n * 2, (unsigned long long)ctx->w4_cvt_limit);
+    two_pass = false;
+  }
+  if (pingpong && m >= kPingPongRows && !two_pass)
     return launch_w4_pingpong(ctx, a, qweight, scales, qzeros, zp_const, y, m, k, n, group, p.out_bf16);
-  if (m >= (pingpong ? kTwoPassRows : kPrefillTwoPassRows) || (m > decode_max && !pow2_group)) {
+  if (two_pass) {
     // W -> bf16 [K][N] (RNE of the exact (q - z) * s: the value the fused
     // kernels round to as well) in the library's conversion buffer, then the
     // NN GEMM with the cost model's config for this shape.

@@ -161,6 +161,7 @@ SIGNATURES = {
     "t0mi_auto_select": (_I, [_U32, _U32, _U32, _CFG]),
     "t0mi_auto_select_legacy": (_I, [_U32, _U32, _U32, _CFG]),
     "t0mi_auto_select_layout": (_I, [_U32, _U32, _U32, _U32, _U32, _CFG]),
+    "t0mi_set_w4a16_workspace_limit": (_I, [_P, _U64]),
     "t0mi_auto_schedule_gemm": (_I, [_U32, _U32, _U32, _U32, _U32, _P, _P, _U32, ctypes.POINTER(_U32)]),
     "t0mi_cached_auto_select": (_I, [_U32, _U32, _U32, _CFG]),
     "t0mi_clear_spec_cache": (None, []),
@@ -667,6 +668,11 @@ class Runtime:
     def w4a16_gemm(self, a: int, qweight: int, scales: int, qzeros: int, zp_const: int, y: int,
                    m: int, k: int, n: int, group: int, out_dtype: int = OUT_BF16) -> None:
         check(lib().t0mi_w4a16_gemm(self.handle, a, qweight, scales, qzeros, zp_const, y, m, k, n, group, out_dtype))
+
+    def set_w4a16_workspace_limit(self, nbytes: int) -> None:
+        """Largest dequantized-weight buffer the W4A16 dequant-once route may use on this runtime;
+        above it the fused kernels run (no reference counterpart)."""
+        check(lib().t0mi_set_w4a16_workspace_limit(self.handle, nbytes))
 
     def dequant_int4(self, qweight: int, scales: int, qzeros: int, zp_const: int, out: int,
                      k: int, n: int, group: int, round_mode: int) -> None:
