@@ -46,13 +46,7 @@ constexpr int PD_CH = 8;      // k-blocks (32 K each) a wave has in flight
 constexpr int PD_ROWS = 32;   // unit rows (two 16-row MFMA blocks)
 constexpr int PD_COLS = 16;   // unit columns (one 16-column MFMA block)
 
-// NN block layout in a wave's LDS: lane l's 16 bytes (K row nn_pd_krow(l), columns
-// 8 * (l & 1) .. +7) are stored at byte 16 * l.
-__device__ __forceinline__ int nn_pd_krow(int l) { return 8 * ((l >> 3) & 3) + 4 * (l >> 5) + ((l & 7) >> 1); }
-// Byte offset of transpose read h (K rows 8 * (l >> 4) + 4 * h + 0..3 of column l % 16).
-__device__ __forceinline__ int nn_pd_tr_off(int l, int h) {
-  return h * 512 + (l >> 4) * 128 + ((l & 15) >> 2) * 32 + (l & 3) * 8;
-}
+// NN block layout in a wave's LDS (nn_pd_krow, nn_pd_tr_off): index_maps.h.
 
 // 16-byte load through the global address space (a generic pointer would become a flat
 // load, which the compiler can only wait for with vmcnt(0) lgkmcnt(0)).

@@ -123,4 +123,16 @@ T0MI_HD constexpr int dec_slot(int h, int r, int x) {
   return 16 * (x >> 1) + ((8 * h + r) ^ (8 * (x & 1) + (x >> 1)));
 }
 
+// Persistent decode kernel, NN: a wave turns a 32 (K) x 16 (column) bf16 block
+// into the 16x16x32 B operand through 1 KB of its own LDS.  Lane l loads 8
+// columns (8 * (l & 1) .. +7) of K row nn_pd_krow(l) and stores the 16 bytes at
+// byte 16 l; the 4-row groups land in the order k = 0-3, 8-11, 16-19, 24-27,
+// 4-7, ..., so that the transpose read h of lane l (K rows 8 (l / 16) + 4 h +
+// 0..3 of column l % 16) starts at nn_pd_tr_off(l, h) and each half-wave's read
+// covers 256 contiguous bytes.
+T0MI_HD constexpr int nn_pd_krow(int l) { return 8 * ((l >> 3) & 3) + 4 * (l >> 5) + ((l & 7) >> 1); }
+T0MI_HD constexpr int nn_pd_tr_off(int l, int h) {
+  return h * 512 + (l >> 4) * 128 + ((l & 15) >> 2) * 32 + (l & 3) * 8;
+}
+
 }  // namespace t0mi

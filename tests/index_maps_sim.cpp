@@ -380,6 +380,48 @@ static void decode_slots() {
     }
 }
 
+// ---- persistent decode kernel, NN block ------------------------------------------
+// Lane l stores 8 columns 8 (l & 1) .. +7 of K row nn_pd_krow(l) at byte 16 l of a 1 KB
+// block.  ds_read_b64_tr_b16 at byte offset o: within each 16-lane group, lane L receives
+// element L % 4 of the 8-byte chunks addressed by lanes 4e + L / 4 (e = 0..3).  The 16x16x32
+// B operand needs, in read h, K rows 8 (L / 16) + 4 h + e of column L % 16.
+static void persistent_nn_block() {
+  std::vector<int> krow_of(1024, -1), col_of(1024, -1);  // per byte pair: K row, column
+  std::set<int> pieces;
+  for (int l = 0; l < 64; ++l) {
+    const int k = nn_pd_krow(l), c0 = 8 * (l & 1);
+    CHECK(k >= 0 && k < 32, "nn_pd_krow(%d) = %d", l, k);
+    pieces.insert(k * 2 + (l & 1));
+    for (int j = 0; j < 8; ++j) {
+      krow_of[16 * l + 2 * j] = k;
+      col_of[16 * l + 2 * j] = c0 + j;
+    }
+  }
+  CHECK(pieces.size() == 64, "NN persistent block stores are not a bijection (%zu pieces)", pieces.size());
+  for (int h = 0; h < 2; ++h) {
+    for (int half = 0; half < 2; ++half) {  // a transpose read is served 32 lanes at a time
+      std::set<int> chunks;
+      int lo = 1 << 30, hi = -1;
+      for (int l = 32 * half; l < 32 * half + 32; ++l) {
+        const int o = nn_pd_tr_off(l, h);
+        CHECK(o >= 0 && o + 8 <= 1024 && o % 8 == 0, "nn_pd_tr_off(%d,%d) = %d", l, h, o);
+        chunks.insert(o / 8);
+        lo = std::min(lo, o);
+        hi = std::max(hi, o + 8);
+      }
+      CHECK(chunks.size() == 32 && hi - lo == 256, "NN persistent tr read h=%d lanes %d-%d: %zu chunks over %d bytes", h,
+            32 * half, 32 * half + 31, chunks.size(), hi - lo);
+    }
+    for (int L = 0; L < 64; ++L)
+      for (int e = 0; e < 4; ++e) {
+        const int src = (L & ~15) + 4 * e + (L & 15) / 4;
+        const int byte = nn_pd_tr_off(src, h) + 2 * (L % 4);
+        CHECK(krow_of[byte] == 8 * (L >> 4) + 4 * h + e && col_of[byte] == (L & 15),
+              "NN persistent read h=%d lane %d element %d finds (k %d, col %d)", h, L, e, krow_of[byte], col_of[byte]);
+      }
+  }
+}
+
 int main() {
   lds_rules();
   printf("%zu LDS rules fit the measurements\n", g_rules.size());
@@ -397,6 +439,7 @@ int main() {
       nn_tile<16>(krows, nw);
       nn_tile<32>(krows, nw);
     }
+  persistent_nn_block();
   pingpong<false>();
   pingpong<true>();
   decode_slots();

@@ -3,7 +3,8 @@ with g++ from rust-gpu_amd/csrc/index_maps.h — the header the kernels include)
 DMA coverage exactly once, LDS bijections, fragment reads finding the chunk the
 MFMA expects (32x32x16 and 16x16x32 operand layouts, the 16x16x32 transpose-read
 lane map), the ping-pong kernel's hoisted per-wave offsets, the W4A16 decode slot
-map, and bank-conflict freedom of the swizzles under every LDS bank rule that
+map, the persistent decode kernel's NN block (stores a bijection, transpose reads
+finding the B operand, each half-wave's read one 256-byte run), and bank-conflict freedom of the swizzles under every LDS bank rule that
 reproduces the conflict counts measured on gfx950 (the measured cycles per read of
 the probe patterns are data in the simulation).  The counterpart of the reference's
 pure-CPU locks in tests/gemm_memory_safety.rs."""
