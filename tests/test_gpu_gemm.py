@@ -355,3 +355,19 @@ def test_reference_k48_tile_dispatch(rt, m):
     dy2, py2 = empty_dev(m * n * 4, fill=0xAB)
     rt.tile_gemm(spec, pa, pb, py2, m, n, k)
     assert np.array_equal(from_dev(dy2, np.float32, (m, n)), ref)
+
+
+@pytest.mark.parametrize("m,n,k,layout", [(128, 1024, 1024, t0mi.NN), (16, 1000, 2048, t0mi.NT),
+                                          (600, 520, 776, t0mi.NN), (3000, 2048, 512, t0mi.NT)])
+def test_ranked_candidates_integer_exact(rt, m, n, k, layout):
+    """Every configuration the cost model ranks in its first 12 for a shape (the candidates
+    GemmTuner times and may pick; cost_model.rs:464-534) computes the exact integer result,
+    split-K partitions included."""
+    nn = layout == t0mi.NN
+    a = oracle.bf16_trunc((((np.arange(m * k) % 7) - 3).astype(np.float32)).reshape(m, k))
+    b = oracle.bf16_trunc((((np.arange(k * n) % 5) - 2).astype(np.float32)).reshape((k, n) if nn else (n, k)))
+    ref = oracle.gemm_bf16(a, b, "nn" if nn else "nt")
+    for cfg, _ in t0mi.auto_schedule_gemm(m, n, k, layout, t0mi.OUT_F32, cap=12):
+        print(f"[gemm] ranked {cfg.name()} {m}x{n}x{k}", flush=True)
+        y = run_gemm(rt, cfg, a, b, m, n, k)
+        assert np.array_equal(y, ref), cfg.name()
