@@ -35,7 +35,7 @@ def parse():
     p.add_argument("--steps", type=int, default=200)
     p.add_argument("--warmup", type=int, default=10)
     p.add_argument("--only", choices=["all", "gemm", "w4a16", "skinny", "prefill", "copy", "dispatch", "stream",
-                                      "mfma", "lds", "vendor", "persistent", "picks"],
+                                      "mfma", "lds", "vendor", "persistent", "picks", "split"],
                    default="all",
                    help="'copy' runs only a plain 1 GiB fp32 copy kernel: the calibration for rocprofv3 "
                         "FETCH_SIZE/WRITE_SIZE readings; 'dispatch' times batched submission (a batch of "
@@ -48,7 +48,8 @@ def parse():
                         "'vendor' times torch.matmul (hipBLASLt) on the BASELINE GEMM shapes beside this "
                         "library's kernels; 'persistent' times the persistent decode preset beside the "
                         "one-shot auto_select configuration; 'picks' times auto_select's pick against the "
-                        "cost model's other top candidates on a set of shapes")
+                        "cost model's other top candidates on a set of shapes; 'split' times the dequant-once "
+                        "W4A16 route with its planned column split against one launch of the head config")
     p.add_argument("--stream-bytes", type=int, default=0,
                    help="with --only stream: bytes per launch (default: the decode's 23,732,224); with "
                         "--stream-calibrate one non-temporal pass over this many bytes")
@@ -772,6 +773,56 @@ def bench_picks(args, torch, t0mi):
                       "higher_is_better": False, "value": round(mean, 4), "results": res}), flush=True)
 
 
+SPLIT_SHAPES = ((4096, 14336, 4096), (1536, 11008, 4096), (2048, 11008, 4096), (1536, 14336, 4096))
+
+
+def bench_split(args, torch, t0mi):
+    """The column split of the auto-scheduled GEMMs (t0mi_auto_gemm_plan) on the dequant-once
+    W4A16 route: per shape, t0mi_w4a16_gemm (dequant to bf16, then the planned pair of launches)
+    against the same dequant followed by one launch of the head configuration over all columns
+    (the schedule without the split).  Operands as the prefill leg (N(0,1) activations, random
+    nibbles and zero points, group 128, bf16 out); median of 5 event-timed batches, the two
+    schedules alternated three times and the middle of those medians kept."""
+    rt = t0mi.Runtime.on_torch_stream(0)
+    g = torch.Generator(device="cuda:0")
+    g.manual_seed(0x7509)
+    G = 128
+    res = []
+    for (m, n, k) in SPLIT_SHAPES:
+        a = torch.randn(m, k, device="cuda:0", generator=g).to(torch.bfloat16)
+        w = torch.randint(-2**31, 2**31 - 1, (k // 8, n), device="cuda:0", dtype=torch.int32, generator=g)
+        s = (torch.rand(k // G, n, device="cuda:0", generator=g) * 0.015 + 0.005).to(torch.bfloat16)
+        z = torch.randint(-2**31, 2**31 - 1, (k // G, n // 8), device="cuda:0", dtype=torch.int32, generator=g)
+        y = torch.empty(m, n, device="cuda:0", dtype=torch.bfloat16)
+        wb = torch.empty(k, n, device="cuda:0", dtype=torch.bfloat16)
+        head, n1, tail = t0mi.auto_gemm_plan(m, n, k, t0mi.NN, t0mi.OUT_BF16)
+        q = (w.data_ptr(), s.data_ptr(), z.data_ptr(), 0)
+
+        def planned(i=0):
+            rt.w4a16_gemm(a.data_ptr(), *q, y.data_ptr(), m, k, n, G, t0mi.OUT_BF16)
+
+        def one_launch(i=0):
+            rt.dequant_int4(*q, wb.data_ptr(), k, n, G, 2)
+            rt.gemm(head, a.data_ptr(), wb.data_ptr(), y.data_ptr(), m, n, k)
+        t = {"planned": [], "one_launch": []}
+        for _ in range(3):
+            for name, f in (("planned", planned), ("one_launch", one_launch)):
+                warm_up(torch, f, 3, min_s=0.1)
+                t[name].append(timed_batches(torch, f, 20)[0])
+        us = {name: sorted(v)[1] for name, v in t.items()}
+        r = {"shape": [m, n, k], "head": head.name(), "n_main": n1, "tail": tail.name() if n1 < n else None,
+             "planned_us": round(us["planned"], 1), "one_launch_us": round(us["one_launch"], 1),
+             "ratio": round(us["planned"] / us["one_launch"], 3)}
+        res.append(r)
+        print(f"[bench] split {m}x{n}x{k}: planned {r['planned_us']} us ({head.name()} to column {n1}"
+              f"{', then ' + r['tail'] if r['tail'] else ''}), one launch {r['one_launch_us']} us",
+              file=sys.stderr, flush=True)
+        del a, w, s, z, y, wb
+    rt.close()
+    print(json.dumps({"metric": "W4A16 dequant-once route: planned column split / one launch", "unit": "ratio",
+                      "higher_is_better": False, "results": res}), flush=True)
+
+
 def bench_dispatch(args, torch, t0mi):
     """Host-visible cost per dispatch of a batch of small GEMMs (the prefill_dispatch.rs
     scenario: dozens of layers x a few kernels), three ways: a synchronous dispatch per
@@ -877,6 +928,9 @@ def main():
         return
     if args.only == "picks":
         bench_picks(args, torch, t0mi)
+        return
+    if args.only == "split":
+        bench_split(args, torch, t0mi)
         return
     rt = t0mi.Runtime.on_torch_stream(0)
     out = {"metric": METRIC, "n_gpus": 1, "steps": args.steps, "warmup": args.warmup, "higher_is_better": True,

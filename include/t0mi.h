@@ -141,6 +141,17 @@ int t0mi_auto_select(uint32_t m, uint32_t k, uint32_t n, t0mi_gemm_config* out);
  * in microseconds.  Writes up to cap entries; *count = the full list length. */
 int t0mi_auto_schedule_gemm(uint32_t m, uint32_t n, uint32_t k, uint32_t transpose, uint32_t out_dtype,
                             t0mi_gemm_config* out, double* est_us, uint32_t cap, uint32_t* count);
+/* The schedule of the library's own auto-scheduled GEMMs (the dequant-once
+ * route of t0mi_w4a16_gemm and the t0mi_matmul_* calls): *head, the ranking's
+ * first prebuilt configuration, over columns [0, *n_main) and, when
+ * *n_main < n, *tail over [*n_main, n) as a second launch.  The split is
+ * planned when head's tiles fill some whole rounds of the GPU and part of one
+ * more and the model expects the pair to be faster (e.g. 4096 x 14336 x 4096 NN:
+ * 256x256 tiles over 12288 columns, the last 2048 on their own tile).  No
+ * reference counterpart (cost_model.rs:464-534 ranks one configuration per
+ * shape); for callers and tests that need to know what runs.  Host only. */
+int t0mi_auto_gemm_plan(uint32_t m, uint32_t n, uint32_t k, uint32_t transpose, uint32_t out_dtype,
+                        t0mi_gemm_config* head, uint32_t* n_main, t0mi_gemm_config* tail);
 /* auto_select_legacy (gemm_gen.rs:351-404), re-derived for gfx950. */
 int t0mi_auto_select_legacy(uint32_t m, uint32_t k, uint32_t n, t0mi_gemm_config* out);
 /* gfx950 extension of auto_select (gemm_gen.rs:340), which only knows the NT

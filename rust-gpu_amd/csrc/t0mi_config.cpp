@@ -229,8 +229,22 @@ bool config_physical(const t0mi_gemm_config& c, t0mi_gemm_config* phys, std::str
 
 // ------------------------------------------------------------- cost model --
 // Analytic time estimate (microseconds) on MI355X for one config.
+// Workgroups of config c one CU holds at once, limited by LDS (160 KB) and by
+// registers (512 per lane, 4 SIMDs); at most 8.
+static double wg_per_cu_of(const t0mi_gemm_config& c) {
+  uint32_t wm = 1, wn = 1;
+  wave_layout(c, &wm, &wn);
+  const double W = wm * wn;
+  const double regs = std::max(64u, est_regs(c));
+  const double waves_per_simd = std::max(1.0, floor(512.0 / regs));
+  const double wg = std::min(floor(160.0 * 1024.0 / lds_total(c)), floor(4.0 * waves_per_simd / W));
+  return std::max(1.0, std::min(wg, 8.0));
+}
+
+static const double kCUs = 256;
+
 static double estimate_us(const t0mi_gemm_config& c, uint32_t m, uint32_t n, uint32_t k) {
-  const double CUS = 256, CLK = 2.4e9, FLOP_PER_CLK_CU = 4096.0;
+  const double CUS = kCUs, CLK = 2.4e9, FLOP_PER_CLK_CU = 4096.0;
   const double HBM = 6.0e12, L2 = 30.0e12;
   uint32_t wm = 1, wn = 1;
   wave_layout(c, &wm, &wn);
@@ -245,11 +259,7 @@ static double estimate_us(const t0mi_gemm_config& c, uint32_t m, uint32_t n, uin
   const uint32_t sk = split_k_of(c);
   const double tm = ceil((double)m / c.tile_m), tn = ceil((double)n / c.tile_n);
   const double tiles = tm * tn * sk;
-  // Workgroups per CU limited by LDS (160 KB) and by registers (512 per lane, 4 SIMDs).
-  const double regs = std::max(64u, est_regs(c));
-  const double waves_per_simd = std::max(1.0, floor(512.0 / regs));
-  double wg_per_cu = std::min(floor(160.0 * 1024.0 / lds_total(c)), floor(4.0 * waves_per_simd / W));
-  wg_per_cu = std::max(1.0, std::min(wg_per_cu, 8.0));
+  const double wg_per_cu = wg_per_cu_of(c);
   const double rounds = ceil(tiles / (CUS * wg_per_cu));
   const double kp = ceil((double)k / sk / c.tile_k) * c.tile_k;
   const double flops_tile = 2.0 * c.tile_m * c.tile_n * kp;
@@ -344,6 +354,31 @@ std::vector<t0mi_gemm_config> rank_candidates(uint32_t m, uint32_t n, uint32_t k
     if (est_us) est_us->push_back(s.first);
   }
   return out;
+}
+
+bool plan_column_split(const t0mi_gemm_config& head, uint32_t m, uint32_t n, uint32_t k, uint32_t transpose,
+                       uint32_t out_dtype, uint32_t* n_main, t0mi_gemm_config* tail) {
+  if (split_k_of(head) > 1 || m == 0 || n == 0 || k == 0) return false;
+  const uint64_t slots = (uint64_t)(kCUs * wg_per_cu_of(head));
+  const uint64_t tm = (m + head.tile_m - 1) / head.tile_m, tn = (n + head.tile_n - 1) / head.tile_n;
+  const uint64_t full_rounds = tm * tn / slots;
+  if (full_rounds == 0 || tm * tn % slots == 0) return false;
+  // Whole columns of tiles that fill whole rounds (at most that many tiles).
+  const uint64_t main_tn = full_rounds * slots / tm;
+  if (main_tn == 0 || main_tn >= tn) return false;
+  const uint32_t n1 = (uint32_t)(main_tn * head.tile_n), n2 = n - n1;
+  std::vector<double> est;
+  const std::vector<t0mi_gemm_config> cands = rank_candidates(m, n2, k, transpose, out_dtype, &est);
+  for (size_t i = 0; i < cands.size(); ++i) {
+    if (!has_variant(cands[i])) continue;
+    // Kept only when the model expects the pair to beat the single launch by more
+    // than a launch's worth.
+    if (estimate_us(head, m, n1, k) + est[i] + 1.0 >= estimate_us(head, m, n, k)) return false;
+    *n_main = n1;
+    *tail = cands[i];
+    return true;
+  }
+  return false;
 }
 
 }  // namespace t0mi

@@ -95,7 +95,8 @@ int ensure_workspace(t0mi_ctx* ctx, size_t bytes);
 // Grows ctx->cvt to at least `bytes` (waits for the stream first).
 int ensure_cvt_buffer(t0mi_ctx* ctx, size_t bytes);
 // Runs a GEMM with the best prebuilt config for (m, n, k, transpose) and the
-// given output type (cost-model ranking, as t0mi_auto_select).  Asynchronous.
+// given output type (cost-model ranking, as t0mi_auto_select), as two launches
+// over column ranges where plan_column_split says so.  Asynchronous.
 int run_gemm_auto(t0mi_ctx* ctx, uint32_t transpose, uint64_t x, uint64_t b, uint64_t y, uint32_t m, uint32_t n,
                   uint32_t k, uint32_t out_dtype = T0MI_OUT_F32, uint64_t bias = 0, const EpiChain* epi = nullptr);
 // Launches the bf16 GEMM kernel for (cfg, params) on ctx's stream.
@@ -115,7 +116,9 @@ int launch_splitk_reduce(t0mi_ctx* ctx, const float* ws, void* y, const float* b
 // The chain of a gemm_gen EpilogueOp.
 EpiChain chain_of(uint32_t gemm_gen_epilogue);
 // Y[m,n] = epi(X . B) with a prebuilt kernel: tile-aligned or not, split-K
-// through the workspace and a deterministic reduce.  Asynchronous.
+// through the workspace and a deterministic reduce.  Asynchronous.  ldn (0: n)
+// is the row length of Y and of NN's B, so that the GEMM can cover a column
+// range of larger matrices (B, Y and bias then point at its first column).
 // A fixed workspace handed to run_gemm in place of ctx->ws: never grown; a
 // GEMM that needs more than `cap` bytes of it is refused before any launch.
 struct FixedWorkspace {
@@ -124,7 +127,7 @@ struct FixedWorkspace {
 };
 int run_gemm(t0mi_ctx* ctx, const t0mi_gemm_config& cfg, const GemmLaunchEntry* e, uint64_t x, uint64_t b,
              uint64_t y, uint64_t bias, uint32_t m, uint32_t n, uint32_t k, const EpiChain& epi,
-             const FixedWorkspace* fixed = nullptr);
+             const FixedWorkspace* fixed = nullptr, uint32_t ldn = 0);
 // True when the chain contains `op`.
 inline bool chain_uses(const EpiChain& e, uint32_t op) {
   for (uint32_t i = 0; i < e.n; ++i)

@@ -43,6 +43,16 @@ bool config_physical(const t0mi_gemm_config& c, t0mi_gemm_config* phys, std::str
 // prebuilt, with split-K options.  Used by auto_select and the tuner.
 std::vector<t0mi_gemm_config> rank_candidates(uint32_t m, uint32_t n, uint32_t k, uint32_t transpose,
                                               uint32_t out_dtype, std::vector<double>* est_us);
+// Column split of an auto-scheduled GEMM whose head candidate (unsplit K) fills
+// some whole rounds of the GPU's workgroup slots and then part of one more: the
+// columns [0, *n_main) of the whole rounds run on `head`, the columns
+// [*n_main, n) as a GEMM of their own on *tail (the ranking's head for that
+// shape, split-K included).  A partly filled last round of large tiles takes
+// nearly a full round's time on a few CUs; the tail's own tile and split spread
+// those columns over the GPU.  True only when the cost model expects the pair
+// of launches to be faster than the single one.
+bool plan_column_split(const t0mi_gemm_config& head, uint32_t m, uint32_t n, uint32_t k, uint32_t transpose,
+                       uint32_t out_dtype, uint32_t* n_main, t0mi_gemm_config* tail);
 
 // ---- tile_ir surface (t0mi_tile.cpp) ----
 // Byte offsets of the epilogue arguments in a TileGemm kernarg (0 = absent)

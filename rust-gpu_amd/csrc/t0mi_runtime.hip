@@ -725,8 +725,10 @@ extern "C" int t0mi_wait_idle(t0mi_ctx* ctx) {
 namespace t0mi {
 int run_gemm(t0mi_ctx* ctx, const t0mi_gemm_config& cfg, const GemmLaunchEntry* e, uint64_t x, uint64_t b,
              uint64_t y, uint64_t bias, uint32_t m, uint32_t n, uint32_t k, const EpiChain& epi,
-             const FixedWorkspace* fixed) {
+             const FixedWorkspace* fixed, uint32_t ldn) {
   if (m == 0 || n == 0) return T0MI_OK;
+  const uint32_t ld = ldn ? ldn : n;
+  if (ld < n || ld % 8) return set_error(T0MI_ERR_INVALID, "row length %u for N=%u", ld, n);
   if (k % 8) return set_error(T0MI_ERR_INVALID, "K=%u must be a multiple of 8", k);
   if (n % 8) return set_error(T0MI_ERR_INVALID, "N=%u must be a multiple of 8", n);
   if ((x | b | y) & 15) return set_error(T0MI_ERR_INVALID, "X, B and Y must be 16-byte aligned");
@@ -742,8 +744,8 @@ int run_gemm(t0mi_ctx* ctx, const t0mi_gemm_config& cfg, const GemmLaunchEntry* 
   p.N = n;
   p.K = k;
   p.lda = k;
-  p.ldb = cfg.transpose == T0MI_NN ? n : k;
-  p.ldy = n;
+  p.ldb = cfg.transpose == T0MI_NN ? ld : k;
+  p.ldy = ld;
   p.tiles_m = (m + cfg.tile_m - 1) / cfg.tile_m;
   p.tiles_n = (n + cfg.tile_n - 1) / cfg.tile_n;
   p.split_k = sk;
@@ -774,7 +776,7 @@ int run_gemm(t0mi_ctx* ctx, const t0mi_gemm_config& cfg, const GemmLaunchEntry* 
     if (ctx->null_backend) return T0MI_OK;
     rc = fill_async(ctx, ws, 0, plane);
     if (rc) return rc;
-    return launch_splitk_reduce(ctx, (const float*)ws, (void*)y, (const float*)bias, m, n, n, 1u, p.out_bf16, epi);
+    return launch_splitk_reduce(ctx, (const float*)ws, (void*)y, (const float*)bias, m, n, ld, 1u, p.out_bf16, epi);
   }
   if (sk == 1) {
     p.k_per_split = k;
@@ -790,7 +792,7 @@ int run_gemm(t0mi_ctx* ctx, const t0mi_gemm_config& cfg, const GemmLaunchEntry* 
   p.y_split_stride = plane;
   rc = launch_gemm(ctx, cfg, e, p);
   if (rc || ctx->null_backend) return rc;
-  return launch_splitk_reduce(ctx, (const float*)ws, (void*)y, (const float*)bias, m, n, n, sk, p.out_bf16, epi);
+  return launch_splitk_reduce(ctx, (const float*)ws, (void*)y, (const float*)bias, m, n, ld, sk, p.out_bf16, epi);
 }
 }  // namespace t0mi
 
@@ -830,15 +832,70 @@ extern "C" int t0mi_gemm_noalloc(t0mi_ctx* ctx, const t0mi_gemm_config* cfg, uin
   return run_gemm(ctx, phys, e, x, b, y, bias, m, n, k, chain_of(cfg->epilogue), &fixed);
 }
 
+namespace {
+// The schedule of an auto-scheduled GEMM: the ranking's first config with a
+// prebuilt kernel over columns [0, *n1) and, when *n1 < n, the planned tail
+// config over [*n1, n).  False when no prebuilt kernel fits.
+struct AutoPlan {
+  t0mi_gemm_config head, tail;
+  const GemmLaunchEntry *e_head = nullptr, *e_tail = nullptr;
+  uint32_t n1 = 0;
+};
+bool auto_plan(uint32_t m, uint32_t n, uint32_t k, uint32_t transpose, uint32_t out_dtype, AutoPlan* pl) {
+  for (const t0mi_gemm_config& c : rank_candidates(m, n, k, transpose, out_dtype, nullptr)) {
+    const GemmLaunchEntry* e = find_gemm_launch(c);
+    if (!e) continue;
+    pl->head = c;
+    pl->e_head = e;
+    pl->n1 = n;
+    uint32_t n1 = 0;
+    t0mi_gemm_config tail;
+    if (plan_column_split(c, m, n, k, transpose, out_dtype, &n1, &tail)) {
+      const GemmLaunchEntry* et = find_gemm_launch(tail);
+      if (et) {
+        pl->tail = tail;
+        pl->e_tail = et;
+        pl->n1 = n1;
+      }
+    }
+    return true;
+  }
+  return false;
+}
+}  // namespace
+
 int t0mi::run_gemm_auto(t0mi_ctx* ctx, uint32_t transpose, uint64_t x, uint64_t b, uint64_t y, uint32_t m, uint32_t n,
                         uint32_t k, uint32_t out_dtype, uint64_t bias, const EpiChain* epi) {
-  const std::vector<t0mi_gemm_config> cands = rank_candidates(m, n, k, transpose, out_dtype, nullptr);
-  for (const t0mi_gemm_config& c : cands) {
-    const GemmLaunchEntry* e = find_gemm_launch(c);
-    if (e) return run_gemm(ctx, c, e, x, b, y, bias, m, n, k, epi ? *epi : EpiChain{});
-  }
-  return set_error(T0MI_ERR_NO_KERNEL, "[t0mi] no prebuilt gfx950 kernel for %ux%ux%u (%s)", m, n, k,
-                   transpose == T0MI_NN ? "NN" : "NT");
+  const EpiChain chain = epi ? *epi : EpiChain{};
+  AutoPlan pl;
+  if (!auto_plan(m, n, k, transpose, out_dtype, &pl))
+    return set_error(T0MI_ERR_NO_KERNEL, "[t0mi] no prebuilt gfx950 kernel for %ux%ux%u (%s)", m, n, k,
+                     transpose == T0MI_NN ? "NN" : "NT");
+  if (pl.n1 == n) return run_gemm(ctx, pl.head, pl.e_head, x, b, y, bias, m, n, k, chain);
+  // Columns [0, n1) on the head config, [n1, n) on the tail's; B, Y and bias
+  // advance to column n1 (NN's B and Y keep their row length n; NT's B rows
+  // are columns).
+  const uint32_t n1 = pl.n1;
+  const uint64_t ob = out_dtype == T0MI_OUT_BF16 ? 2 : 4;
+  int rc = run_gemm(ctx, pl.head, pl.e_head, x, b, y, bias, m, n1, k, chain, nullptr, n);
+  if (rc) return rc;
+  const uint64_t b_tail = b + (transpose == T0MI_NN ? (uint64_t)n1 * 2 : (uint64_t)n1 * k * 2);
+  return run_gemm(ctx, pl.tail, pl.e_tail, x, b_tail, y + (uint64_t)n1 * ob, bias ? bias + (uint64_t)n1 * 4 : 0, m,
+                  n - n1, k, chain, nullptr, n);
+}
+
+extern "C" int t0mi_auto_gemm_plan(uint32_t m, uint32_t n, uint32_t k, uint32_t transpose, uint32_t out_dtype,
+                                   t0mi_gemm_config* head, uint32_t* n_main, t0mi_gemm_config* tail) {
+  if (!head || !n_main || !tail) return set_error(T0MI_ERR_INVALID, "null output");
+  if (!m || !n || !k) return set_error(T0MI_ERR_INVALID, "zero dimension");
+  if (transpose > T0MI_NN || out_dtype > T0MI_OUT_BF16) return set_error(T0MI_ERR_INVALID, "bad layout or out_dtype");
+  AutoPlan pl;
+  if (!auto_plan(m, n, k, transpose, out_dtype, &pl))
+    return set_error(T0MI_ERR_NO_KERNEL, "[t0mi] no prebuilt gfx950 kernel for %ux%ux%u", m, n, k);
+  *head = pl.head;
+  *n_main = pl.n1;
+  *tail = pl.n1 < n ? pl.tail : pl.head;
+  return T0MI_OK;
 }
 
 // ------------------------------------------------------------ tile_ir GEMM ----

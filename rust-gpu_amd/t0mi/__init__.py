@@ -163,6 +163,7 @@ SIGNATURES = {
     "t0mi_auto_select_layout": (_I, [_U32, _U32, _U32, _U32, _U32, _CFG]),
     "t0mi_set_w4a16_workspace_limit": (_I, [_P, _U64]),
     "t0mi_auto_schedule_gemm": (_I, [_U32, _U32, _U32, _U32, _U32, _P, _P, _U32, ctypes.POINTER(_U32)]),
+    "t0mi_auto_gemm_plan": (_I, [_U32, _U32, _U32, _U32, _U32, _CFG, ctypes.POINTER(_U32), _CFG]),
     "t0mi_cached_auto_select": (_I, [_U32, _U32, _U32, _CFG]),
     "t0mi_clear_spec_cache": (None, []),
     "t0mi_spec_cache_len": (_SZ, []),
@@ -374,6 +375,16 @@ def auto_schedule_gemm(m: int, n: int, k: int, transpose: int = NN, out_dtype: i
     check(lib().t0mi_auto_schedule_gemm(m, n, k, transpose, out_dtype, ctypes.cast(cfgs, _P), ctypes.cast(est, _P),
                                         cap, ctypes.byref(count)))
     return [(cfgs[i].copy(), est[i]) for i in range(min(cap, count.value))]
+
+
+def auto_gemm_plan(m: int, n: int, k: int, transpose: int = NN, out_dtype: int = OUT_F32):
+    """The schedule of the library's auto-scheduled GEMMs: (head, n_main, tail) -- head over columns
+    [0, n_main), tail over [n_main, n) when n_main < n (tail is head otherwise)."""
+    head, tail = GemmConfig(), GemmConfig()
+    n_main = ctypes.c_uint32(0)
+    check(lib().t0mi_auto_gemm_plan(m, n, k, transpose, out_dtype, ctypes.byref(head), ctypes.byref(n_main),
+                                    ctypes.byref(tail)))
+    return head, n_main.value, tail
 
 
 def auto_select_legacy(m: int, k: int, n: int) -> GemmConfig:

@@ -149,6 +149,36 @@ def test_auto_schedule_gemm_ranking():
         t0mi.auto_schedule_gemm(0, 64, 64)
 
 
+def test_auto_gemm_plan_column_split():
+    """The column split of the library's auto-scheduled GEMMs: the head is the ranking's first
+    entry; a split only where the head's tiles fill whole rounds of the GPU (256 CUs x the tile's
+    workgroups per CU) and part of one more, after the most whole columns of tiles that fit in
+    the whole rounds; the tail is the ranking's head for the remaining columns."""
+    cases = {  # (m, n, k, layout) -> the first column of the tail (n: no split)
+        (4096, 14336, 4096, t0mi.NN): 12288,     # BASELINE config 5's GEMM: 896 tiles = 3.5 rounds
+        (1536, 11008, 4096, t0mi.NN): 10752,     # 258 tiles: 252 of them fill one round
+        (4096, 4352, 1024, t0mi.NT): 4096,
+        (4096, 4096, 4096, t0mi.NN): 4096,       # whole rounds: nothing to split
+        (4096, 11008, 4096, t0mi.NN): 11008,     # last round 69 % full: the model keeps one launch
+        (768, 11008, 4096, t0mi.NN): 11008,      # under one round
+        (128, 4096, 4096, t0mi.NN): 4096,        # split-K head: never split
+    }
+    for (m, n, k, tr), want in cases.items():
+        head, n1, tail = t0mi.auto_gemm_plan(m, n, k, tr, t0mi.OUT_BF16)
+        ranked = t0mi.auto_schedule_gemm(m, n, k, tr, t0mi.OUT_BF16, cap=1)
+        assert head.name() == ranked[0][0].name()
+        assert n1 == want, ((m, n, k, tr), n1)
+        if n1 == n:
+            assert tail.name() == head.name()
+            continue
+        tm, tn = -(-m // head.tile_m), -(-n // head.tile_n)
+        whole = (tm * tn // 256) * 256  # tiles of the whole rounds
+        assert n1 % head.tile_n == 0 and whole - tm < tm * (n1 // head.tile_n) <= whole
+        assert tail.name() == t0mi.auto_schedule_gemm(m, n - n1, k, tr, t0mi.OUT_BF16, cap=1)[0][0].name()
+    with pytest.raises(t0mi.T0miError):
+        t0mi.auto_gemm_plan(0, 64, 64)
+
+
 def test_auto_select_legacy():
     """gemm_gen.rs:636-646: small squares use split-K with tile_m 64; 1024^3 uses tile_m 128."""
     c = t0mi.auto_select_legacy(256, 256, 256)
