@@ -773,7 +773,8 @@ def bench_picks(args, torch, t0mi):
                       "higher_is_better": False, "value": round(mean, 4), "results": res}), flush=True)
 
 
-SPLIT_SHAPES = ((4096, 14336, 4096), (1536, 11008, 4096), (2048, 11008, 4096), (1536, 14336, 4096))
+SPLIT_SHAPES = ((4096, 14336, 4096), (1536, 11008, 4096), (2048, 11008, 4096), (1536, 14336, 4096),
+                (2048, 14336, 4096))
 
 
 def bench_split(args, torch, t0mi):

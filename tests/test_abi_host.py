@@ -157,6 +157,8 @@ def test_auto_gemm_plan_column_split():
     cases = {  # (m, n, k, layout) -> the first column of the tail (n: no split)
         (4096, 14336, 4096, t0mi.NN): 12288,     # BASELINE config 5's GEMM: 896 tiles = 3.5 rounds
         (1536, 11008, 4096, t0mi.NN): 10752,     # 258 tiles: 252 of them fill one round
+        (2048, 14336, 4096, t0mi.NN): 14336,     # 448 tiles, last round 75 % full: one launch
+        (3072, 14336, 4096, t0mi.NN): 14336,     # 672 tiles: two whole rounds, last 62.5 % full
         (4096, 4352, 1024, t0mi.NT): 4096,
         (4096, 4096, 4096, t0mi.NN): 4096,       # whole rounds: nothing to split
         (4096, 11008, 4096, t0mi.NN): 11008,     # last round 69 % full: the model keeps one launch
