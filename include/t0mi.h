@@ -443,7 +443,9 @@ int t0mi_auto_gemm(t0mi_ctx* ctx, uint64_t a, uint64_t b, uint64_t c, uint32_t m
  * kernel, 192..1535 rows (K and group multiples of 64) the 256x256 ping-pong
  * kernel, K split through the library workspace when tiles are fewer than
  * CUs; from 1536 rows (768 when K or the group is not a multiple of 64, and
- * from 81 rows for a group that is not a power of two) the weight is
+ * from 81 rows for a group that is not a power of two; from 1025 rows when the
+ * ping-pong tiles overflow one round of the GPU and t0mi_auto_gemm_plan splits
+ * the dense GEMM's columns) the weight is
  * dequantized once to bf16 into the library's conversion buffer (k * n * 2
  * bytes, kept by the runtime) and the dense NN GEMM runs, unless that is above
  * the runtime's limit (t0mi_set_w4a16_workspace_limit).  The ping-pong and the

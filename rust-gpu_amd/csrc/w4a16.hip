@@ -345,7 +345,9 @@ static int hip_fail(hipError_t e, const char* what) {
 //    the weights are dequantized once to bf16 and the dense NN GEMM runs: the
 //    dequant pass (0.5 B read + 2 B written per weight, at HBM speed) then costs
 //    less than dequantizing inside every M tile's K-loop, which is VALU work
-//    (2048 rows: 224 us two-pass against 232 us fused; 4096 rows: 414 vs 457).
+//    (2048 rows: 224 us two-pass against 232 us fused; 4096 rows: 414 vs 457);
+//    and from kSplitRouteRows + 1 rows on when the fused kernel's tiles overflow
+//    one round and the dense GEMM's plan splits the columns.
 static constexpr uint32_t kDecodeMaxRows = 80;    // groups the one-slab decode kernels take
 // Groups 32..256: up to kDecodeMaxLaunches multi-slab launches (N = 11008: three
 // launches of four slabs, 191 rows, 47 us against 47 for the 128x128 kernel; two
@@ -357,6 +359,7 @@ static constexpr uint32_t kDecodeMaxLaunches = 3;
 static uint32_t decode_max_slabs(uint32_t group) { return group == 256 ? 2 : group == 128 ? 4 : 3; }
 static constexpr uint32_t kPingPongRows = 192;
 static constexpr uint32_t kTwoPassRows = 1536;
+static constexpr uint32_t kSplitRouteRows = 1024;
 static constexpr uint32_t kPrefillTwoPassRows = 768;  // groups or K the ping-pong kernel does not take
 
 static int launch_dequant(t0mi_ctx* ctx, uint64_t qweight, uint64_t scales, uint64_t qzeros, uint32_t zp_const,
@@ -471,6 +474,20 @@ extern "C" int t0mi_w4a16_gemm(t0mi_ctx* ctx, uint64_t a, uint64_t qweight, uint
   const uint32_t decode_max = v2_group ? 16 * decode_max_slabs(group) * kDecodeMaxLaunches : kDecodeMaxRows;
   const bool pingpong = w4_pingpong_ok(k, group, 1, k);
   bool two_pass = m >= (pingpong ? kTwoPassRows : kPrefillTwoPassRows) || (m > decode_max && !pow2_group);
+  if (!two_pass && pingpong && m > kSplitRouteRows) {
+    // The fused ping-pong kernel's 256 x 256 tiles overflow one round of the
+    // GPU: where the dense GEMM's plan splits the columns instead (whole rounds
+    // on 256 x 256, the rest on their own tile), dequant-once runs that plan
+    // (1280 x 14336 x 4096: 179 us against 208.5 fused).  Below kSplitRouteRows
+    // rows the dequant pass costs more than the split saves (768 x 28672:
+    // 215 against 204 us).
+    const uint64_t tiles = (uint64_t)((m + 255) / 256) * ((n + 255) / 256);
+    t0mi_gemm_config head, tail;
+    uint32_t n_main = n;
+    if (tiles > (uint64_t)ctx->cu_count &&
+        t0mi_auto_gemm_plan(m, n, k, T0MI_NN, out_dtype, &head, &n_main, &tail) == T0MI_OK && n_main < n)
+      two_pass = true;
+  }
   if (two_pass && (uint64_t)k * n * 2 > ctx->w4_cvt_limit) {
     // The caller's limit on the conversion buffer: dequantize inside the K loop instead.
     if (!pingpong && !pow2_group)

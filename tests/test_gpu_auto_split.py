@@ -90,3 +90,40 @@ def test_w4a16_two_pass_split_k_tail(rt):
     ref = oracle.gemm_bf16(a, np.ascontiguousarray(wb[:, cols]), "nn", nthreads=8)
     # bf16 output: each element rounded once more (relative 2^-9 at most)
     check_close(oracle.bf16_to_f32(y[:, cols]), ref, a, wb[:, cols], k, rel_max=3e-3)
+
+
+def test_w4a16_fused_size_takes_split_plan(rt):
+    """1280 rows (under the dequant-once threshold of 1536): the fused ping-pong kernel's 280
+    tiles of 256 x 256 would overflow one round, and the dense GEMM's plan splits the columns,
+    so the call runs dequant-once with that plan: bit-identical to dequant + one launch of the
+    head config (the tail is unsplit), and within the GEMM tolerance of the fused route that a
+    zero workspace limit forces (a different K split for the same sums)."""
+    m, k, n, group = 1280, 1024, 14336, 128
+    head, n1, tail = t0mi.auto_gemm_plan(m, n, k, t0mi.NN, t0mi.OUT_BF16)
+    assert n1 < n and tail.split_k in (0, 1), (head.name(), n1, tail.name())
+    a = oracle.normal_bf16((m, k), 0xC1, 0.0, 1.0)
+    w = oracle.pack_qweight(oracle.nibbles((k, n), 0xC2))
+    s = oracle.uniform_bf16((k // group, n), 0xC3, 0.005, 0.02)
+    z = oracle.pack_qzeros(oracle.nibbles((k // group, n), 0xC4))
+    bufs = [to_dev(v) for v in (a, w, s, z)]
+    (_, pa), (_, pw), (_, ps), (_, pz) = bufs
+    print(f"[auto split] w4a16 {m}x{k}x{n} g{group}: {head.name()} to column {n1}, then {tail.name()}", flush=True)
+    outs = []
+    for limit in (2**64 - 1, 0):
+        rt.set_w4a16_workspace_limit(limit)
+        dy, py = empty_dev(m * n * 2, fill=0xCD)
+        rt.w4a16_gemm(pa, pw, ps, pz, 0, py, m, k, n, group, t0mi.OUT_BF16)
+        outs.append(from_dev(dy, np.uint16, (m, n)))
+    rt.set_w4a16_workspace_limit(2**64 - 1)
+    y, y_fused = outs
+    dwb, pwb = empty_dev(k * n * 2)
+    rt.dequant_int4(pw, ps, pz, 0, pwb, k, n, group, 2)
+    dy1, py1 = empty_dev(m * n * 2, fill=0xAB)
+    rt.gemm(head.copy(transpose=t0mi.NN, out_dtype=t0mi.OUT_BF16), pa, pwb, py1, m, n, k)
+    y1 = from_dev(dy1, np.uint16, (m, n))
+    assert np.array_equal(y, y1), f"{np.count_nonzero(y != y1)} elements differ"
+    wb = oracle.bf16_rne(oracle.dequant_qweight_f32(w, s, z, group, 0))
+    rows = slice(m - 32, m)
+    ref = oracle.gemm_bf16(np.ascontiguousarray(a[rows]), wb, "nn", nthreads=8)
+    for out in (y, y_fused):
+        check_close(oracle.bf16_to_f32(out[rows]), ref, a[rows], wb, k, rel_max=3e-3)
