@@ -34,30 +34,19 @@ def parse():
     p.add_argument("--gpus", type=int, default=1)
     p.add_argument("--steps", type=int, default=200)
     p.add_argument("--warmup", type=int, default=10)
-    p.add_argument("--only", choices=["all", "gemm", "w4a16", "skinny", "prefill", "copy", "dispatch", "stream",
-                                      "mfma", "lds", "vendor", "persistent", "picks", "split"],
+    p.add_argument("--only", choices=["all", "gemm", "w4a16", "skinny", "prefill", "shard", "copy", "dispatch",
+                                      "persistent", "split"],
                    default="all",
-                   help="'copy' runs only a plain 1 GiB fp32 copy kernel: the calibration for rocprofv3 "
-                        "FETCH_SIZE/WRITE_SIZE readings; 'dispatch' times batched submission (a batch of "
-                        "small GEMM dispatches: synchronous, DispatchQueue, HIP graph); 'skinny' and "
-                        "'prefill' time BASELINE configs 3 and 5 (parity shapes, not the headline line); "
-                        "'stream' times the probe floors of the W4A16 decode (a streaming read of its bytes "
-                        "over rotated copies, and an empty launch); 'mfma' MFMA loops of the GEMM wave tiles "
-                        "(32x32x16 / 16x16x32, operands in registers or re-read from LDS) with their shader "
-                        "clocks; 'lds' one launch per LDS read pattern (for rocprofv3 bank-conflict counters); "
-                        "'vendor' times torch.matmul (hipBLASLt) on the BASELINE GEMM shapes beside this "
-                        "library's kernels; 'persistent' times the persistent decode preset beside the "
-                        "one-shot auto_select configuration; 'picks' times auto_select's pick against the "
-                        "cost model's other top candidates on a set of shapes; 'split' times the dequant-once "
-                        "W4A16 route with its planned column split against one launch of the head config")
-    p.add_argument("--stream-bytes", type=int, default=0,
-                   help="with --only stream: bytes per launch (default: the decode's 23,732,224); with "
-                        "--stream-calibrate one non-temporal pass over this many bytes")
-    p.add_argument("--stream-calibrate", action="store_true",
-                   help="with --only stream: run only non-temporal 16-byte read passes of --stream-bytes "
-                        "(default 1 GiB), the FETCH_SIZE calibration for the decode's load type")
+                   help="'copy' runs only a plain 1 GiB fp32 copy kernel (torch): the calibration for "
+                        "rocprofv3 FETCH_SIZE/WRITE_SIZE readings; 'dispatch' times batched submission (a "
+                        "batch of small GEMM dispatches: synchronous, DispatchQueue, HIP graph); 'gemm', "
+                        "'w4a16', 'skinny', 'prefill' and 'shard' time one leg of the default run alone "
+                        "(BASELINE configs 2, 4, 3, 5 and the 1376-column W4A16 decode shard); 'persistent' "
+                        "times the persistent decode preset beside the one-shot auto_select configuration; "
+                        "'split' times the dequant-once W4A16 route with its planned column split against "
+                        "one launch of the head config")
     p.add_argument("--clocks", action="store_true",
-                   help="with --only gemm / w4a16 / mfma: sample the GPU clock and power (amd-smi) during ~3 s of "
+                   help="with --only gemm / w4a16: sample the GPU clock and power (amd-smi) during ~3 s of "
                         "sustained launches and report their medians")
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     p.add_argument("--config", default=None, help="GEMM preset name to force (default: auto_select)")
@@ -451,232 +440,6 @@ def smi_sample(duration_s, launch, torch):
             "samples": len(use), "clock_MHz_samples": [round(c) for c, _ in use]}
 
 
-def bench_stream(args, torch):
-    """Probe floors of the W4A16 decode: one streaming read of its algorithmic bytes per
-    launch (16-byte loads, non-temporal and normal; rotated over >= 512 MB of copies, as
-    the decode's weights are), at several grid sizes, and an empty launch."""
-    from t0mi import probes
-    stream_ptr = torch.cuda.current_stream().cuda_stream
-    sink = torch.zeros(1 << 16, device="cuda:0", dtype=torch.int32)
-    if args.stream_calibrate:
-        nbytes = args.stream_bytes or (1 << 30)
-        buf = torch.zeros(nbytes, device="cuda:0", dtype=torch.uint8)
-        for _ in range(max(1, args.steps)):
-            probes.stream(stream_ptr, buf.data_ptr(), nbytes, True, 2048, sink.data_ptr())
-        torch.cuda.synchronize()
-        print(json.dumps({"calibration": "non-temporal 16-byte streaming read", "read_bytes": nbytes,
-                          "launches": max(1, args.steps)}), flush=True)
-        return
-    nbytes = args.stream_bytes or 23732224
-    nbytes -= nbytes % 16
-    copies = max(2, -(-512 * 1024 * 1024 // nbytes))
-    buf = torch.zeros(copies * nbytes, device="cuda:0", dtype=torch.uint8)
-    base = buf.data_ptr()
-    calls = max(args.steps * 4, 2 * copies)
-    res = {}
-    for nt in (True, False):
-        for grid in (256, 512, 1024, 2048):
-            launch = lambda i, nt=nt, grid=grid: probes.stream(stream_ptr, base + (i % copies) * nbytes, nbytes, nt,
-                                                              grid, sink.data_ptr())
-            warm_up(torch, lambda: launch(0), args.warmup)
-            us, batches = timed_batches(torch, launch, calls)
-            res[f"{'nt' if nt else 'normal'}_grid{grid}"] = {"us": round(us, 3),
-                                                              "GB/s": round(nbytes / (us * 1e-6) / 1e9, 1),
-                                                              "batch_us": [round(b, 3) for b in batches]}
-    empty = {}
-    for grid in (172, 256, 1024):
-        launch = lambda i, grid=grid: probes.empty(stream_ptr, grid, sink.data_ptr())
-        warm_up(torch, lambda: launch(0), args.warmup)
-        us, batches = timed_batches(torch, launch, calls)
-        empty[f"grid{grid}"] = {"us": round(us, 3), "batch_us": [round(b, 3) for b in batches]}
-    best = min(res.items(), key=lambda kv: kv[1]["us"])
-    # The same launches replayed from a HIP graph: no host enqueue cost between them (a
-    # Python-driven launch costs ~3 us of host time, more than an empty kernel's GPU time).
-    best_nt = best[0].startswith("nt")
-    best_grid = int(best[0].split("grid")[1])
-    side = torch.cuda.Stream()
-    graphs = {}
-    with torch.cuda.stream(side):
-        for name, fn, n in (("stream_" + best[0], lambda k: probes.stream(side.cuda_stream, base + (k % copies) * nbytes,
-                                                                          nbytes, best_nt, best_grid, sink.data_ptr()),
-                             4 * copies),
-                            ("empty_grid256", lambda k: probes.empty(side.cuda_stream, 256, sink.data_ptr()), 200)):
-            gr = torch.cuda.CUDAGraph()
-            torch.cuda.synchronize()
-            with torch.cuda.graph(gr, stream=side):
-                for k in range(n):
-                    fn(k)
-            torch.cuda.synchronize()
-            vals = []
-            for rep in range(3 + BATCHES):
-                e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-                e0.record(side)
-                gr.replay()
-                e1.record(side)
-                torch.cuda.synchronize()
-                if rep >= 3:
-                    vals.append(e0.elapsed_time(e1) * 1e3 / n)
-            vals.sort()
-            graphs[name] = {"us": round(vals[len(vals) // 2], 3), "launches_per_replay": n,
-                            "replay_us_per_launch": [round(v, 3) for v in vals]}
-    g_us = graphs["stream_" + best[0]]["us"]
-    print(json.dumps({"metric": "streaming-read floor of the W4A16 decode's bytes", "unit": "us/launch",
-                      "higher_is_better": False, "bytes_per_launch": nbytes, "copies_rotated": copies,
-                      "launches_per_batch": calls, "timing": f"median of {BATCHES} batches (HIP events)",
-                      "best": {"case": best[0], **best[1]},
-                      "graph_replay": graphs,
-                      "floor_GB/s_graph": round(nbytes / (g_us * 1e-6) / 1e9, 1),
-                      "floor_frac_graph": round(nbytes / (g_us * 1e-6) / 1e9 / PEAK_HBM_GBS, 4),
-                      "stream": res, "empty_kernel_256_threads": empty}),
-          flush=True)
-
-
-def bench_mfma(args, torch):
-    """MFMA loops (t0mi_probes.hip probe_mfma, 256 workgroups): the ping-pong kernel's wave
-    tile (8 waves x 128x64, 32x32x16) and a 4-wave 128x128 tile with 32x32x16 or 16x16x32,
-    operands held in registers or re-read from LDS each k-step, on random N(0,1) bf16 (and
-    zeros for the ping-pong tile): TFLOP/s and the shader clock from s_memtime /
-    s_memrealtime (100 MHz) stamps; with --clocks also amd-smi clock and power."""
-    from t0mi import probes
-    stream_ptr = torch.cuda.current_stream().cuda_stream
-    n_frag, grid, iters = 1 << 16, 256, 4000
-    g = torch.Generator(device="cuda:0")
-    g.manual_seed(0x7701)
-    srcs = {"random": torch.randn(n_frag * 8, device="cuda:0", generator=g).to(torch.bfloat16),
-            "zero": torch.zeros(n_frag * 8, device="cuda:0", dtype=torch.bfloat16)}
-    out = torch.empty(grid * 512, device="cuda:0", dtype=torch.float32)
-    stamps = torch.zeros(grid * 4, device="cuda:0", dtype=torch.int64)
-    res = {}
-    runs = [(0, "zero")] + [(v, "random") for v in sorted(probes.MFMA_VARIANTS)]
-    for variant, data in runs:
-        src = srcs[data]
-        flop = grid * iters * probes.mfma_flop_per_iter(variant)
-        launch = lambda i=0, src=src, v=variant: probes.mfma(stream_ptr, src.data_ptr(), n_frag, iters, grid,
-                                                             out.data_ptr(), stamps.data_ptr(), v)
-        warm_up(torch, lambda: launch(), 2, min_s=1.0)
-        us, batches = timed_batches(torch, launch, 20)
-        st = stamps.view(grid, 4).cpu().numpy().astype("float64")
-        clk = (st[:, 1] - st[:, 0]) / (st[:, 3] - st[:, 2]) * 100.0  # MHz: shader cycles per 10 ns tick
-        clk.sort()
-        name = f"v{variant}_{data}"
-        res[name] = {"variant": probes.MFMA_VARIANTS[variant][0], "operands": data,
-                     "us_per_launch": round(us, 1), "TFLOP/s": round(flop / (us * 1e-6) / 1e12, 1),
-                     "frac_of_peak": round(flop / (us * 1e-6) / 1e12 / PEAK_BF16_TFLOPS, 4),
-                     "shader_clock_MHz_median": round(float(clk[len(clk) // 2]), 1),
-                     "batch_us": [round(b, 1) for b in batches]}
-        if args.clocks:
-            res[name]["amd_smi"] = smi_sample(3.0, launch, torch)
-        print(f"[bench] mfma {name}: {res[name]['TFLOP/s']} TFLOP/s at {res[name]['shader_clock_MHz_median']} MHz"
-              + (f", {res[name]['amd_smi']['power_W_median']} W" if args.clocks else ""), file=sys.stderr, flush=True)
-    print(json.dumps({"metric": "MFMA loops of a GEMM wave tile", "unit": "TFLOP/s",
-                      "workload": f"{grid} workgroups x {iters} iterations (64 of K) of the wave tile's MFMAs",
-                      "peak": PEAK_BF16_TFLOPS, "results": res}), flush=True)
-
-
-def lds_patterns():
-    """Lane -> LDS byte offset tables of one ds_read_b128 (64 lanes): the operand layouts of
-    the GEMM kernels (rows of 64 K = 128 bytes; 32x32x16: lane l reads row l % 32, chunk
-    l / 32; 16x16x32: row l % 16, chunk l / 16) under their swizzles, and probes that put
-    two lanes differing in one index bit on the same bank at different addresses."""
-    swz = lambda r: (r ^ ((r >> 3) & 3)) & 7
-    far = lambda l: 16384 + 16 * l
-    pats = [("contiguous", [16 * l for l in range(64)]),
-            ("x32_swz", [(l % 32) * 128 + ((l // 32) ^ swz(l % 32)) * 16 for l in range(64)]),
-            ("x16_swz", [(l % 16) * 128 + ((l // 16) ^ swz(l % 16)) * 16 for l in range(64)]),
-            ("x16_rot", [(l % 16) * 128 + ((l // 16 + l % 16) % 8) * 16 for l in range(64)]),
-            ("x16_none", [(l % 16) * 128 + (l // 16) * 16 for l in range(64)]),
-            ("x16_swz_lanes0-15_only", [(l % 16) * 128 + ((l // 16) ^ swz(l % 16)) * 16 if l < 16 else far(l)
-                                        for l in range(64)]),
-            # rows of 32 K (64 bytes, 4 chunks), chunks 0-1 and 2-3: the former swizzle
-            # (r / 2 ^ (r >> 3) & 3) & 3, then the one the kernels use now, (r >> 2) & 3
-            ("x32_k32_old_c0", [(l % 32) * 64 + ((l // 32) ^ ((l % 32 // 2 ^ (l % 32 >> 3) & 3) & 3)) * 16
-                                for l in range(64)]),
-            ("x32_k32_old_c2", [(l % 32) * 64 + ((2 + l // 32) ^ ((l % 32 // 2 ^ (l % 32 >> 3) & 3) & 3)) * 16
-                                for l in range(64)]),
-            ("x32_k32_swz_c0", [(l % 32) * 64 + ((l // 32) ^ ((l % 32 >> 2) & 3)) * 16 for l in range(64)]),
-            ("x32_k32_swz_c2", [(l % 32) * 64 + ((2 + l // 32) ^ ((l % 32 >> 2) & 3)) * 16 for l in range(64)])]
-    x16 = lambda l: (l % 16) * 128 + ((l // 16) ^ swz(l % 16)) * 16
-    x32 = lambda l: (l % 32) * 128 + ((l // 32) ^ swz(l % 32)) * 16
-    pats += [("x16_swz_lanes16-31_only", [x16(l) if 16 <= l < 32 else far(l) for l in range(64)]),
-             ("x16_swz_lanes0-15_32-47_only", [x16(l) if (l & 31) < 16 else far(l) for l in range(64)]),
-             ("x32_swz_lanes0-31_only", [x32(l) if l < 32 else far(l) for l in range(64)]),
-             ("chunk_major_16_rows", [(l // 16) * 256 + (l % 16) * 16 for l in range(64)]),
-             ("lanes0-15_stride32", [32 * l if l < 16 else far(l) for l in range(64)]),
-             ("lanes0-31_interleaved_stride32", [32 * l if l < 16 else 32 * (l - 16) + 16 if l < 32 else far(l)
-                                                 for l in range(64)]),
-             ("lanes16-31_4096_apart", [16 * l if l < 16 else 16 * (l - 16) + 4096 if l < 32 else far(l)
-                                        for l in range(64)])]
-    for b in range(6):
-        for d in ((1024,) if b in (1, 2) else (256, 512, 1024)):
-            pats.append((f"bit{b}_same_bank_{d}_apart", [(l & ~(1 << b)) * 16 + ((l >> b) & 1) * d for l in range(64)]))
-    return pats
-
-
-def bench_lds(args, torch):
-    """One launch per lane -> address pattern of lds_patterns() (t0mi_probe_lds: 256
-    workgroups x 8 waves x 2000 dependent ds_read_b128), in the order listed.  Under
-    rocprofv3 --pmc SQ_LDS_BANK_CONFLICT SQ_LDS_IDX_ACTIVE SQ_INSTS_LDS each dispatch's
-    counters give the LDS cycles per read of its pattern (4 when conflict-free)."""
-    from t0mi import probes
-    stream_ptr = torch.cuda.current_stream().cuda_stream
-    out = torch.empty(256 * 512, device="cuda:0", dtype=torch.int32)
-    res = []
-    for name, tab in lds_patterns():
-        t = torch.tensor(tab, dtype=torch.int32, device="cuda:0")
-        launch = lambda: probes.lds(stream_ptr, t.data_ptr(), 16, 2000, 256, out.data_ptr())
-        launch()
-        torch.cuda.synchronize()
-        t0 = time.perf_counter()
-        launch()
-        torch.cuda.synchronize()
-        res.append({"name": name, "us_per_launch": round((time.perf_counter() - t0) * 1e6, 1)})
-        print(f"[bench] lds {len(res) - 1} {name}", file=sys.stderr, flush=True)
-    print(json.dumps({"metric": "LDS read patterns (ds_read_b128), one launch each, in order", "unit": "us",
-                      "patterns": res}), flush=True)
-
-
-def bench_vendor(args, torch, t0mi):
-    """torch.matmul (hipBLASLt on ROCm) against t0mi_gemm on BASELINE configs 2 and 3 and
-    the NT form of config 2, same operands (N(0,1) / N(0,0.02) bf16, bf16 out), same
-    timing (median of 5 event-timed batches on torch's current stream); B of config 3 is
-    rotated over 16 copies as in --only skinny."""
-    rt = t0mi.Runtime.on_torch_stream(0)
-    g = torch.Generator(device="cuda:0")
-    g.manual_seed(0x7801)
-    res = {}
-    cases = (("config2_4096_NN", 4096, 4096, 4096, 1.0, t0mi.NN, 1),
-             ("config2_4096_NT", 4096, 4096, 4096, 1.0, t0mi.NT, 1),
-             ("config3_128x4096x4096_NN", 128, 4096, 4096, 0.02, t0mi.NN, 16))
-    for name, m, n, k, sd, tr, copies in cases:
-        a = (torch.randn(m, k, device="cuda:0", generator=g) * sd).to(torch.bfloat16)
-        shape_b = (k, n) if tr == t0mi.NN else (n, k)
-        bs = [(torch.randn(*shape_b, device="cuda:0", generator=g) * sd).to(torch.bfloat16) for _ in range(copies)]
-        y = torch.empty(m, n, device="cuda:0", dtype=torch.bfloat16)
-        cfg = t0mi.auto_select_layout(m, k, n, tr, t0mi.OUT_BF16).copy(transpose=tr, out_dtype=t0mi.OUT_BF16)
-        pa, py = a.data_ptr(), y.data_ptr()
-        bp = [b.data_ptr() for b in bs]
-        ours = lambda i: rt.gemm(cfg, pa, bp[i % copies], py, m, n, k)
-        if tr == t0mi.NN:
-            theirs = lambda i: torch.matmul(a, bs[i % copies], out=y)
-        else:
-            bts = [b.t() for b in bs]  # a transposed view: torch picks the NT kernel
-            theirs = lambda i: torch.matmul(a, bts[i % copies], out=y)
-        row = {}
-        for who, fn in (("t0mi", ours), ("torch.matmul", theirs)):
-            warm_up(torch, lambda fn=fn: fn(0), args.warmup)
-            us, batches = timed_batches(torch, fn, max(args.steps, 2 * copies))
-            row[who] = {"us": round(us, 2), "TFLOP/s": round(2.0 * m * n * k / (us * 1e-6) / 1e12, 1),
-                        "batch_us": [round(b, 2) for b in batches]}
-        row["t0mi_kernel"] = cfg.name()
-        row["speedup"] = round(row["torch.matmul"]["us"] / row["t0mi"]["us"], 3)
-        res[name] = row
-        print(f"[bench] vendor {name}: t0mi {row['t0mi']['us']} us, torch.matmul {row['torch.matmul']['us']} us "
-              f"(x{row['speedup']})", file=sys.stderr, flush=True)
-    rt.close()
-    print(json.dumps({"metric": "t0mi_gemm vs torch.matmul (hipBLASLt), us per call", "unit": "us",
-                      "higher_is_better": False, "torch": torch.__version__, "results": res}), flush=True)
-
-
 def bench_persistent(args, torch, t0mi):
     """The persistent preset tile_persistent_decode (tile_ir.rs:540-561) through t0mi_tile_gemm: one
     launch of the persistent decode kernel, beside the one-shot configuration the cost model picks
@@ -724,53 +487,6 @@ def bench_persistent(args, torch, t0mi):
     rt.close()
     print(json.dumps({"metric": "tile_persistent_decode vs the one-shot auto_select config, us per call",
                       "unit": "us", "higher_is_better": False, "results": res}), flush=True)
-
-
-PICK_SHAPES = ((1, 4096, 4096), (16, 4096, 4096), (64, 4096, 4096), (128, 4096, 4096), (256, 4096, 4096),
-               (16, 11008, 4096), (32, 11008, 4096), (512, 11008, 4096), (512, 512, 512), (1024, 1024, 1024),
-               (2048, 2048, 2048), (1024, 4096, 4096), (768, 11008, 4096), (1536, 11008, 4096),
-               (2048, 11008, 4096), (1536, 14336, 4096))
-
-
-def bench_picks(args, torch, t0mi):
-    """auto_select's pick (the head of cost_model::auto_schedule_gemm, cost_model.rs:464-534) against
-    the model's next candidates, per shape: NN, bf16 out, N(0,1) bf16, B rotated over >= 256 MB,
-    median of 3 event-timed batches; 4- and 5-stage copies of a 3-stage tile are skipped."""
-    rt = t0mi.Runtime.on_torch_stream(0)
-    g = torch.Generator(device="cuda:0")
-    g.manual_seed(3)
-    res = []
-    for (m, n, k) in PICK_SHAPES:
-        ranked = t0mi.auto_schedule_gemm(m, n, k, t0mi.NN, t0mi.OUT_BF16, cap=64)
-        cands, seen = [], set()
-        for c, e in ranked:
-            key = (c.tile_m, c.tile_n, c.tile_k, c.wave_m, c.wave_n, c.split_k)
-            if c.stages in (4, 5) and key in seen:
-                continue
-            seen.add(key)
-            cands.append((c, e))
-            if len(cands) == 10:
-                break
-        copies = max(2, -(-(256 << 20) // (2 * n * k)))
-        a = torch.randn(m, k, device="cuda:0", generator=g).to(torch.bfloat16)
-        bs = [torch.randn(k, n, device="cuda:0", generator=g).to(torch.bfloat16) for _ in range(copies)]
-        y = torch.empty(m, n, device="cuda:0", dtype=torch.bfloat16)
-        rows = []
-        for c, e in cands:
-            f = lambda i, c=c: rt.gemm(c, a.data_ptr(), bs[i % copies].data_ptr(), y.data_ptr(), m, n, k)
-            warm_up(torch, lambda: f(0), 4, min_s=0.05)
-            us, _ = timed_batches(torch, f, max(60, 2 * copies), batches=3)
-            rows.append({"config": c.name(), "est_us": round(e, 2), "us": round(us, 2)})
-        best = min(rows, key=lambda r: r["us"])
-        res.append({"shape": [m, n, k], "pick": rows[0], "best": best,
-                    "pick_over_best": round(rows[0]["us"] / best["us"], 3), "candidates": rows})
-        print(f"[bench] picks {m}x{n}x{k}: pick {rows[0]['config']} {rows[0]['us']} us, best {best['config']} "
-              f"{best['us']} us", file=sys.stderr, flush=True)
-        del a, bs, y
-    rt.close()
-    mean = sum(r["pick_over_best"] for r in res) / len(res)
-    print(json.dumps({"metric": "auto_select pick / fastest of the cost model's top candidates", "unit": "ratio",
-                      "higher_is_better": False, "value": round(mean, 4), "results": res}), flush=True)
 
 
 SPLIT_SHAPES = ((4096, 14336, 4096), (1536, 11008, 4096), (2048, 11008, 4096), (1536, 14336, 4096),
@@ -908,27 +624,12 @@ def main():
     if args.only == "copy":
         copy_calibration(args, torch)
         return
-    if args.only == "stream":
-        bench_stream(args, torch)
-        return
-    if args.only == "mfma":
-        bench_mfma(args, torch)
-        return
-    if args.only == "lds":
-        bench_lds(args, torch)
-        return
     import t0mi
     if args.only == "dispatch":
         bench_dispatch(args, torch, t0mi)
         return
-    if args.only == "vendor":
-        bench_vendor(args, torch, t0mi)
-        return
     if args.only == "persistent":
         bench_persistent(args, torch, t0mi)
-        return
-    if args.only == "picks":
-        bench_picks(args, torch, t0mi)
         return
     if args.only == "split":
         bench_split(args, torch, t0mi)

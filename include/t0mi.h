@@ -190,10 +190,31 @@ int t0mi_null_inject_timeout(t0mi_ctx* ctx);
 /* Null runtime only: grid (work-items) and kernarg bytes of the last dispatch. */
 int t0mi_null_last_dispatch(t0mi_ctx* ctx, uint32_t grid[3], uint8_t* ka, size_t ka_cap, size_t* ka_len);
 
-/* GpuRuntime::alloc / alloc_zero / recycle / read_f32 / write (gpu_context.rs:508-545). */
+/* GpuRuntime::alloc (gpu_context.rs:508-510) through its BufferPool
+ * (gpu_context.rs:31-90): the size is rounded up to 4096 bytes, the pool key; a
+ * buffer recycled at that size is handed out again, zeroed in stream order
+ * before any later work on the runtime's stream; otherwise a fresh allocation
+ * (contents undefined).  Not during graph capture when it must allocate. */
 int t0mi_alloc(t0mi_ctx* ctx, size_t bytes, uint64_t* dptr);
+/* GpuRuntime::alloc_zero (gpu_context.rs:513-517): alloc, zeroed, and waits. */
 int t0mi_alloc_zero(t0mi_ctx* ctx, size_t bytes, uint64_t* dptr);
+/* GpuRuntime::alloc_f32 (gpu_context.rs:520-525): n floats, max(4n, 512) bytes
+ * rounded up to 512, from the pool, zeroed in stream order. */
+int t0mi_alloc_f32(t0mi_ctx* ctx, size_t n, uint64_t* dptr);
+/* GpuRuntime::recycle (gpu_context.rs:528-531): the buffer returns to the pool
+ * (no wait, no free); queued work that uses it still runs before its next
+ * hand-out, which zeroes it in stream order. */
+int t0mi_recycle(t0mi_ctx* ctx, uint64_t dptr);
+/* BufferPool::cached_bytes / clear (gpu_context.rs:83-93); clear waits for the
+ * stream, then frees every pooled buffer. */
+size_t t0mi_pool_cached_bytes(t0mi_ctx* ctx);
+int t0mi_pool_clear(t0mi_ctx* ctx);
+/* Frees a buffer now (after the stream's queued work): no reference counterpart
+ * (the reference's GpuBuffer frees on drop). */
 int t0mi_free(t0mi_ctx* ctx, uint64_t dptr);
+/* GpuBuffer::write / read behind GpuRuntime::write_f32 / read_f32
+ * (gpu_context.rs:536-552): synchronous copies; read_f32 waits for the stream
+ * first, as here. */
 int t0mi_h2d(t0mi_ctx* ctx, uint64_t dst, const void* src, size_t bytes);
 int t0mi_d2h(t0mi_ctx* ctx, void* dst, uint64_t src, size_t bytes);
 int t0mi_memset(t0mi_ctx* ctx, uint64_t dst, int value, size_t bytes);
@@ -458,11 +479,15 @@ int t0mi_w4a16_gemm(t0mi_ctx* ctx, uint64_t a, uint64_t qweight, uint64_t scales
  * that cannot hold the dequantized weight (k * n * 2 bytes of the runtime's
  * conversion buffer): t0mi_w4a16_gemm calls on this runtime whose dequant-once
  * route would need more than `bytes` run the fused kernels instead -- the
- * 256x256 ping-pong kernel (K and group multiples of 64) or the 128x128 fused
- * tile kernel (other power-of-two groups), the weights crossing HBM once, at 4
- * bits; with a group that is neither, such calls return T0MI_ERR_INVALID.
- * Results are those of the default route (the ping-pong kernel's are
- * bit-identical to dequant-once).  Default: no limit.  0: never dequantize once. */
+ * 256x256 ping-pong kernel (K and group multiples of 64, any row count from
+ * 192 on, and from 81 rows for a group that is not a power of two) or the
+ * 128x128 fused tile kernel (other power-of-two groups), the weights crossing
+ * HBM once, at 4 bits; with a group that is neither, such calls return
+ * T0MI_ERR_INVALID.  Every route rounds each weight (q - z) * s once to bf16;
+ * the fused results are bit-identical to dequant-once where the dense GEMM
+ * takes the same 256x256 tile and K partitions (4096 rows and more: config 5),
+ * and otherwise within the GEMM tolerance of them (another tile or K split sums
+ * in another order).  Default: no limit.  0: never dequantize once. */
 int t0mi_set_w4a16_workspace_limit(t0mi_ctx* ctx, uint64_t bytes);
 
 /* Standalone dequant, replacing build_dequant_int4_{f32,bf16} (quant_kernels.rs:53-171)

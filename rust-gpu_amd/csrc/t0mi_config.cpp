@@ -357,9 +357,9 @@ std::vector<t0mi_gemm_config> rank_candidates(uint32_t m, uint32_t n, uint32_t k
 }
 
 bool plan_column_split(const t0mi_gemm_config& head, uint32_t m, uint32_t n, uint32_t k, uint32_t transpose,
-                       uint32_t out_dtype, uint32_t* n_main, t0mi_gemm_config* tail) {
-  if (split_k_of(head) > 1 || m == 0 || n == 0 || k == 0) return false;
-  const uint64_t slots = (uint64_t)(kCUs * wg_per_cu_of(head));
+                       uint32_t out_dtype, uint32_t* n_main, t0mi_gemm_config* tail, uint32_t cus) {
+  if (split_k_of(head) > 1 || m == 0 || n == 0 || k == 0 || cus == 0) return false;
+  const uint64_t slots = (uint64_t)(cus * wg_per_cu_of(head));
   const uint64_t tm = (m + head.tile_m - 1) / head.tile_m, tn = (n + head.tile_n - 1) / head.tile_n;
   const uint64_t full_rounds = tm * tn / slots;
   if (full_rounds == 0 || tm * tn % slots == 0) return false;

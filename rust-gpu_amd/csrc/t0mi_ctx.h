@@ -55,7 +55,11 @@ struct t0mi_ctx {
   uint32_t timeout_ms = 60000;  // aql.rs:481-545: 60 s
   std::mutex mu;
   std::map<std::string, std::unique_ptr<t0mi_kernel>> kernels;  // name -> kernel (ensure_kernel_t0 cache)
-  std::map<uint64_t, size_t> allocs;                            // live t0mi_alloc buffers
+  std::map<uint64_t, size_t> allocs;                            // live t0mi_alloc buffers (pool-aligned size)
+  // BufferPool (gpu_context.rs:31-90): recycled buffers by 4096-aligned size,
+  // handed out again (zeroed) by t0mi_alloc / t0mi_alloc_f32; cached bytes.
+  std::map<size_t, std::vector<uint64_t>> pool;
+  size_t pool_bytes = 0;
   // Held by every call that launches work or uses ws / cvt, so a runtime can be
   // shared between threads (launches reach the stream in lock order).
   // Recursive: entry points call each other.  Waits run outside it.
@@ -99,6 +103,21 @@ int ensure_cvt_buffer(t0mi_ctx* ctx, size_t bytes);
 // over column ranges where plan_column_split says so.  Asynchronous.
 int run_gemm_auto(t0mi_ctx* ctx, uint32_t transpose, uint64_t x, uint64_t b, uint64_t y, uint32_t m, uint32_t n,
                   uint32_t k, uint32_t out_dtype = T0MI_OUT_F32, uint64_t bias = 0, const EpiChain* epi = nullptr);
+// The schedule of an auto-scheduled GEMM: the ranking's first config with a
+// prebuilt kernel over columns [0, n1) and, when n1 < n, the planned tail
+// config over [n1, n) (plan_column_split with `cus` compute units).  False
+// when no prebuilt kernel fits.  Host only.
+struct AutoPlan {
+  t0mi_gemm_config head, tail;
+  const GemmLaunchEntry *e_head = nullptr, *e_tail = nullptr;
+  uint32_t n1 = 0;
+};
+bool auto_plan(uint32_t m, uint32_t n, uint32_t k, uint32_t transpose, uint32_t out_dtype, uint32_t cus,
+               AutoPlan* pl);
+// Runs a plan made by auto_plan for the same (m, n, k, transpose, out_dtype).
+int run_gemm_planned(t0mi_ctx* ctx, const AutoPlan& pl, uint32_t transpose, uint64_t x, uint64_t b, uint64_t y,
+                     uint32_t m, uint32_t n, uint32_t k, uint32_t out_dtype = T0MI_OUT_F32, uint64_t bias = 0,
+                     const EpiChain* epi = nullptr);
 // Launches the bf16 GEMM kernel for (cfg, params) on ctx's stream.
 int launch_gemm(t0mi_ctx* ctx, const t0mi_gemm_config& cfg, const GemmLaunchEntry* e, GemmParams p);
 int check_ctx(t0mi_ctx* ctx);

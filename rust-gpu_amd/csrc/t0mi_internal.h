@@ -50,9 +50,10 @@ std::vector<t0mi_gemm_config> rank_candidates(uint32_t m, uint32_t n, uint32_t k
 // shape, split-K included).  A partly filled last round of large tiles takes
 // nearly a full round's time on a few CUs; the tail's own tile and split spread
 // those columns over the GPU.  True only when the cost model expects the pair
-// of launches to be faster than the single one.
+// of launches to be faster than the single one.  `cus`: the GPU's compute
+// units (the workgroup slots of a round).
 bool plan_column_split(const t0mi_gemm_config& head, uint32_t m, uint32_t n, uint32_t k, uint32_t transpose,
-                       uint32_t out_dtype, uint32_t* n_main, t0mi_gemm_config* tail);
+                       uint32_t out_dtype, uint32_t* n_main, t0mi_gemm_config* tail, uint32_t cus = 256);
 
 // ---- tile_ir surface (t0mi_tile.cpp) ----
 // Byte offsets of the epilogue arguments in a TileGemm kernarg (0 = absent)

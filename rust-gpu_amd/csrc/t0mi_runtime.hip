@@ -370,6 +370,8 @@ extern "C" void t0mi_ctx_destroy(t0mi_ctx* ctx) {
     (void)hipSetDevice(ctx->device);
     if (!ctx->poisoned.load()) (void)hipStreamSynchronize(ctx->stream);
     for (auto& kv : ctx->allocs) (void)hipFree((void*)kv.first);
+    for (auto& kv : ctx->pool)
+      for (uint64_t p : kv.second) (void)hipFree((void*)p);
     if (ctx->ws) (void)hipFree(ctx->ws);
     if (ctx->cvt) (void)hipFree(ctx->cvt);
     if (ctx->own_stream) (void)hipStreamDestroy(ctx->stream);
@@ -402,17 +404,103 @@ extern "C" int t0mi_null_last_dispatch(t0mi_ctx* ctx, uint32_t grid[3], uint8_t*
 
 // ---------------------------------------------------------------- memory ----
 
+// BufferPool::alloc (gpu_context.rs:54-73): the size rounded up to 4096 bytes
+// is the pool key; a recycled buffer of that size is handed out again, zeroed
+// on the stream before any later work (a fill kernel, so that no stale
+// contents reach the next user), else a fresh one is allocated (contents
+// undefined, as the reference's alloc_vram).
+static int pool_alloc(t0mi_ctx* ctx, size_t bytes, uint64_t* dptr, bool* reused) {
+  const size_t aligned = ((bytes ? bytes : 1) + 4095) / 4096 * 4096;
+  uint64_t p = 0;
+  {
+    std::lock_guard<std::mutex> lk(ctx->mu);
+    auto it = ctx->pool.find(aligned);
+    if (it != ctx->pool.end() && !it->second.empty()) {
+      p = it->second.back();
+      it->second.pop_back();
+      ctx->pool_bytes -= aligned;
+      ctx->allocs[p] = aligned;
+    }
+  }
+  *reused = p != 0;
+  if (p) {
+    T0MI_SUBMIT_GUARD(ctx);
+    int rc = fill_async(ctx, (void*)p, 0, aligned);
+    if (rc) return rc;
+    *dptr = p;
+    return T0MI_OK;
+  }
+  if (int rc = refuse_if_capturing(ctx, "t0mi_alloc")) return rc;
+  void* q = nullptr;
+  hipError_t e = hipMalloc(&q, aligned);
+  if (e != hipSuccess) return hip_fail(e, "hipMalloc");
+  std::lock_guard<std::mutex> lk(ctx->mu);
+  ctx->allocs[(uint64_t)q] = aligned;
+  *dptr = (uint64_t)q;
+  return T0MI_OK;
+}
+
 extern "C" int t0mi_alloc(t0mi_ctx* ctx, size_t bytes, uint64_t* dptr) {
   if (!ctx || !dptr) return set_error(T0MI_ERR_INVALID, "null argument");
   if (ctx->null_backend) return set_error(T0MI_ERR_NO_DEVICE, "null runtime has no memory");
-  if (int rc = refuse_if_capturing(ctx, "t0mi_alloc")) return rc;
-  void* p = nullptr;
-  hipError_t e = hipMalloc(&p, bytes ? bytes : 1);
-  if (e != hipSuccess) return hip_fail(e, "hipMalloc");
+  bool reused = false;
+  return pool_alloc(ctx, bytes, dptr, &reused);
+}
+
+// GpuRuntime::alloc_f32 (gpu_context.rs:520-525): n floats, at least 512 bytes,
+// rounded up to 512, zeroed (in stream order).
+extern "C" int t0mi_alloc_f32(t0mi_ctx* ctx, size_t n, uint64_t* dptr) {
+  if (!ctx || !dptr) return set_error(T0MI_ERR_INVALID, "null argument");
+  if (ctx->null_backend) return set_error(T0MI_ERR_NO_DEVICE, "null runtime has no memory");
+  if (n > (SIZE_MAX - 511) / 4) return set_error(T0MI_ERR_INVALID, "n=%zu floats overflow", n);
+  const size_t bytes = (std::max<size_t>(n * 4, 512) + 511) & ~(size_t)511;
+  bool reused = false;
+  int rc = pool_alloc(ctx, bytes, dptr, &reused);
+  if (rc || reused) return rc;  // a recycled buffer is zeroed by pool_alloc
+  T0MI_SUBMIT_GUARD(ctx);
+  return fill_async(ctx, (void*)*dptr, 0, (bytes + 4095) / 4096 * 4096);
+}
+
+// GpuRuntime::recycle / BufferPool::recycle (gpu_context.rs:76-81, 528-531):
+// the buffer goes back to the pool under its aligned size; nothing waits and
+// nothing is freed.  Work already queued on the stream that uses it still
+// runs first: the buffer's next hand-out is zeroed in stream order after it.
+extern "C" int t0mi_recycle(t0mi_ctx* ctx, uint64_t dptr) {
+  if (!ctx) return set_error(T0MI_ERR_INVALID, "null runtime");
   std::lock_guard<std::mutex> lk(ctx->mu);
-  ctx->allocs[(uint64_t)p] = bytes;
-  *dptr = (uint64_t)p;
+  auto it = ctx->allocs.find(dptr);
+  if (it == ctx->allocs.end())
+    return set_error(T0MI_ERR_INVALID, "pointer 0x%llx was not allocated by t0mi_alloc", (unsigned long long)dptr);
+  ctx->pool[it->second].push_back(dptr);
+  ctx->pool_bytes += it->second;
+  ctx->allocs.erase(it);
   return T0MI_OK;
+}
+
+// BufferPool::cached_bytes (gpu_context.rs:90-93).
+extern "C" size_t t0mi_pool_cached_bytes(t0mi_ctx* ctx) {
+  if (!ctx) return 0;
+  std::lock_guard<std::mutex> lk(ctx->mu);
+  return ctx->pool_bytes;
+}
+
+// BufferPool::clear (gpu_context.rs:83-88): frees every cached buffer (after
+// the stream's queued work, which may still use them).
+extern "C" int t0mi_pool_clear(t0mi_ctx* ctx) {
+  if (!ctx) return set_error(T0MI_ERR_INVALID, "null runtime");
+  if (ctx->null_backend) return T0MI_OK;
+  if (int rc = refuse_if_capturing(ctx, "t0mi_pool_clear")) return rc;
+  (void)hipStreamSynchronize(ctx->stream);
+  std::lock_guard<std::mutex> lk(ctx->mu);
+  hipError_t first = hipSuccess;
+  for (auto& kv : ctx->pool)
+    for (uint64_t p : kv.second) {
+      hipError_t e = hipFree((void*)p);
+      if (first == hipSuccess) first = e;
+    }
+  ctx->pool.clear();
+  ctx->pool_bytes = 0;
+  return first == hipSuccess ? T0MI_OK : hip_fail(first, "hipFree");
 }
 
 extern "C" int t0mi_alloc_zero(t0mi_ctx* ctx, size_t bytes, uint64_t* dptr) {
@@ -832,16 +920,8 @@ extern "C" int t0mi_gemm_noalloc(t0mi_ctx* ctx, const t0mi_gemm_config* cfg, uin
   return run_gemm(ctx, phys, e, x, b, y, bias, m, n, k, chain_of(cfg->epilogue), &fixed);
 }
 
-namespace {
-// The schedule of an auto-scheduled GEMM: the ranking's first config with a
-// prebuilt kernel over columns [0, *n1) and, when *n1 < n, the planned tail
-// config over [*n1, n).  False when no prebuilt kernel fits.
-struct AutoPlan {
-  t0mi_gemm_config head, tail;
-  const GemmLaunchEntry *e_head = nullptr, *e_tail = nullptr;
-  uint32_t n1 = 0;
-};
-bool auto_plan(uint32_t m, uint32_t n, uint32_t k, uint32_t transpose, uint32_t out_dtype, AutoPlan* pl) {
+bool t0mi::auto_plan(uint32_t m, uint32_t n, uint32_t k, uint32_t transpose, uint32_t out_dtype, uint32_t cus,
+                     AutoPlan* pl) {
   for (const t0mi_gemm_config& c : rank_candidates(m, n, k, transpose, out_dtype, nullptr)) {
     const GemmLaunchEntry* e = find_gemm_launch(c);
     if (!e) continue;
@@ -850,7 +930,7 @@ bool auto_plan(uint32_t m, uint32_t n, uint32_t k, uint32_t transpose, uint32_t 
     pl->n1 = n;
     uint32_t n1 = 0;
     t0mi_gemm_config tail;
-    if (plan_column_split(c, m, n, k, transpose, out_dtype, &n1, &tail)) {
+    if (plan_column_split(c, m, n, k, transpose, out_dtype, &n1, &tail, cus)) {
       const GemmLaunchEntry* et = find_gemm_launch(tail);
       if (et) {
         pl->tail = tail;
@@ -862,15 +942,20 @@ bool auto_plan(uint32_t m, uint32_t n, uint32_t k, uint32_t transpose, uint32_t 
   }
   return false;
 }
-}  // namespace
 
 int t0mi::run_gemm_auto(t0mi_ctx* ctx, uint32_t transpose, uint64_t x, uint64_t b, uint64_t y, uint32_t m, uint32_t n,
                         uint32_t k, uint32_t out_dtype, uint64_t bias, const EpiChain* epi) {
-  const EpiChain chain = epi ? *epi : EpiChain{};
   AutoPlan pl;
-  if (!auto_plan(m, n, k, transpose, out_dtype, &pl))
+  if (!auto_plan(m, n, k, transpose, out_dtype, (uint32_t)ctx->cu_count, &pl))
     return set_error(T0MI_ERR_NO_KERNEL, "[t0mi] no prebuilt gfx950 kernel for %ux%ux%u (%s)", m, n, k,
                      transpose == T0MI_NN ? "NN" : "NT");
+  return run_gemm_planned(ctx, pl, transpose, x, b, y, m, n, k, out_dtype, bias, epi);
+}
+
+int t0mi::run_gemm_planned(t0mi_ctx* ctx, const AutoPlan& pl, uint32_t transpose, uint64_t x, uint64_t b, uint64_t y,
+                           uint32_t m, uint32_t n, uint32_t k, uint32_t out_dtype, uint64_t bias,
+                           const EpiChain* epi) {
+  const EpiChain chain = epi ? *epi : EpiChain{};
   if (pl.n1 == n) return run_gemm(ctx, pl.head, pl.e_head, x, b, y, bias, m, n, k, chain);
   // Columns [0, n1) on the head config, [n1, n) on the tail's; B, Y and bias
   // advance to column n1 (NN's B and Y keep their row length n; NT's B rows
@@ -890,7 +975,7 @@ extern "C" int t0mi_auto_gemm_plan(uint32_t m, uint32_t n, uint32_t k, uint32_t 
   if (!m || !n || !k) return set_error(T0MI_ERR_INVALID, "zero dimension");
   if (transpose > T0MI_NN || out_dtype > T0MI_OUT_BF16) return set_error(T0MI_ERR_INVALID, "bad layout or out_dtype");
   AutoPlan pl;
-  if (!auto_plan(m, n, k, transpose, out_dtype, &pl))
+  if (!auto_plan(m, n, k, transpose, out_dtype, 256, &pl))
     return set_error(T0MI_ERR_NO_KERNEL, "[t0mi] no prebuilt gfx950 kernel for %ux%ux%u", m, n, k);
   *head = pl.head;
   *n_main = pl.n1;

@@ -474,6 +474,10 @@ extern "C" int t0mi_w4a16_gemm(t0mi_ctx* ctx, uint64_t a, uint64_t qweight, uint
   const uint32_t decode_max = v2_group ? 16 * decode_max_slabs(group) * kDecodeMaxLaunches : kDecodeMaxRows;
   const bool pingpong = w4_pingpong_ok(k, group, 1, k);
   bool two_pass = m >= (pingpong ? kTwoPassRows : kPrefillTwoPassRows) || (m > decode_max && !pow2_group);
+  // The dense GEMM's schedule, planned once (with this GPU's CU count) and run
+  // by the dequant-once route below when it is taken.
+  AutoPlan plan;
+  bool planned = false;
   if (!two_pass && pingpong && m > kSplitRouteRows) {
     // The fused ping-pong kernel's 256 x 256 tiles overflow one round of the
     // GPU: where the dense GEMM's plan splits the columns instead (whole rounds
@@ -482,12 +486,12 @@ extern "C" int t0mi_w4a16_gemm(t0mi_ctx* ctx, uint64_t a, uint64_t qweight, uint
     // rows the dequant pass costs more than the split saves (768 x 28672:
     // 215 against 204 us).
     const uint64_t tiles = (uint64_t)((m + 255) / 256) * ((n + 255) / 256);
-    t0mi_gemm_config head, tail;
-    uint32_t n_main = n;
-    if (tiles > (uint64_t)ctx->cu_count &&
-        t0mi_auto_gemm_plan(m, n, k, T0MI_NN, out_dtype, &head, &n_main, &tail) == T0MI_OK && n_main < n)
-      two_pass = true;
+    if (tiles > (uint64_t)ctx->cu_count) {
+      planned = auto_plan(m, n, k, T0MI_NN, out_dtype, (uint32_t)ctx->cu_count, &plan);
+      if (planned && plan.n1 < n) two_pass = true;
+    }
   }
+  bool fused_only = false;  // the caller's limit turned the dequant-once route off
   if (two_pass && (uint64_t)k * n * 2 > ctx->w4_cvt_limit) {
     // The caller's limit on the conversion buffer: dequantize inside the K loop instead.
     if (!pingpong && !pow2_group)
@@ -496,8 +500,13 @@ extern "C" int t0mi_w4a16_gemm(t0mi_ctx* ctx, uint64_t a, uint64_t qweight, uint
                        "of %llu bytes (no fused kernel takes this group)",
                        m, group, (unsigned long long)k * n * 2, (unsigned long long)ctx->w4_cvt_limit);
     two_pass = false;
+    fused_only = true;
   }
-  if (pingpong && m >= kPingPongRows && !two_pass)
+  // The ping-pong kernel takes any group that is a multiple of 64 and any M
+  // (rows past M load zeros); below kPingPongRows it runs only for groups the
+  // 128x128 fused kernel cannot index (not a power of two) once the limit has
+  // ruled out dequant-once.
+  if (pingpong && !two_pass && (m >= kPingPongRows || (fused_only && !pow2_group && m > decode_max)))
     return launch_w4_pingpong(ctx, a, qweight, scales, qzeros, zp_const, y, m, k, n, group, p.out_bf16);
   if (two_pass) {
     // W -> bf16 [K][N] (RNE of the exact (q - z) * s: the value the fused
@@ -507,9 +516,14 @@ extern "C" int t0mi_w4a16_gemm(t0mi_ctx* ctx, uint64_t a, uint64_t qweight, uint
     if (rc) return rc;
     rc = launch_dequant(ctx, qweight, scales, qzeros, zp_const, (uint64_t)ctx->cvt, k, n, group, 2);
     if (rc) return rc;
+    if (planned) return run_gemm_planned(ctx, plan, T0MI_NN, a, (uint64_t)ctx->cvt, y, m, n, k, out_dtype);
     return run_gemm_auto(ctx, T0MI_NN, a, (uint64_t)ctx->cvt, y, m, n, k, out_dtype);
   }
-  if (m > decode_max) {  // power-of-two group here
+  if (m > decode_max) {
+    // The 128x128 fused kernel indexes scales and zero points by k >> log2(group).
+    if (!pow2_group)
+      return set_error(T0MI_ERR_INVALID, "internal: %u rows with group %u reached the power-of-two fused kernel", m,
+                       group);
     // Many rows: dequant fused into the MFMA K-loop, weights read once per tile column.
     W4PrefillParams q;
     memset(&q, 0, sizeof q);

@@ -180,6 +180,10 @@ SIGNATURES = {
     "t0mi_alloc": (_I, [_P, _SZ, ctypes.POINTER(_U64)]),
     "t0mi_alloc_zero": (_I, [_P, _SZ, ctypes.POINTER(_U64)]),
     "t0mi_free": (_I, [_P, _U64]),
+    "t0mi_alloc_f32": (_I, [_P, _SZ, ctypes.POINTER(_U64)]),
+    "t0mi_recycle": (_I, [_P, _U64]),
+    "t0mi_pool_cached_bytes": (_SZ, [_P]),
+    "t0mi_pool_clear": (_I, [_P]),
     "t0mi_h2d": (_I, [_P, _U64, _P, _SZ]),
     "t0mi_d2h": (_I, [_P, _P, _U64, _SZ]),
     "t0mi_memset": (_I, [_P, _U64, _I, _SZ]),
@@ -622,6 +626,22 @@ class Runtime:
 
     def free(self, dptr: int):
         check(lib().t0mi_free(self.handle, dptr))
+
+    def alloc_f32(self, n: int) -> int:
+        """``GpuRuntime::alloc_f32``: n floats (at least 512 bytes, rounded to 512), zeroed."""
+        p = ctypes.c_uint64()
+        check(lib().t0mi_alloc_f32(self.handle, n, ctypes.byref(p)))
+        return p.value
+
+    def recycle(self, dptr: int):
+        """``GpuRuntime::recycle``: back to the pool, no wait, no free."""
+        check(lib().t0mi_recycle(self.handle, dptr))
+
+    def pool_cached_bytes(self) -> int:
+        return lib().t0mi_pool_cached_bytes(self.handle)
+
+    def pool_clear(self):
+        check(lib().t0mi_pool_clear(self.handle))
 
     def h2d(self, dptr: int, host_bytes) -> None:
         import numpy as np

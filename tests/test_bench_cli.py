@@ -48,27 +48,3 @@ def test_leg_prints_one_json_line(leg, unit, bound):
     assert roof["bound"] == bound and 0 < roof["frac"] < 1
     assert roof["frac"] == pytest.approx(roof["achieved"] / roof["peak"], rel=1e-3)
     assert roof["traffic"] > 0
-
-
-@pytest.mark.gpu
-def test_probe_floors_print_one_json_line():
-    """--only stream / mfma / lds (libt0mi_probes.so): the decode's streaming-read and
-    empty-launch floors, the MFMA loops' rates with their shader clocks, and the LDS
-    bank-pattern launches."""
-    r = run_bench("--only", "stream", "--steps", "12", "--warmup", "2")
-    assert r.returncode == 0, r.stderr[-2000:]
-    out = json.loads(r.stdout.strip().splitlines()[-1])
-    assert out["bytes_per_launch"] == 23732224 and out["copies_rotated"] * out["bytes_per_launch"] >= 512 << 20
-    assert 0 < out["best"]["us"] < 1000 and all(v["us"] > 0 for v in out["empty_kernel_256_threads"].values())
-    r = run_bench("--only", "mfma", "--steps", "2", "--warmup", "1")
-    assert r.returncode == 0, r.stderr[-2000:]
-    res = json.loads(r.stdout.strip().splitlines()[-1])["results"]
-    assert {"v0_zero", "v0_random", "v5_random", "v7_random"} <= set(res)
-    for v in res.values():
-        assert 0 < v["frac_of_peak"] < 1.05 and 100 < v["shader_clock_MHz_median"] < 3000
-    r = run_bench("--only", "lds")
-    assert r.returncode == 0, r.stderr[-2000:]
-    out = json.loads(r.stdout.strip().splitlines()[-1])
-    names = [p["name"] for p in out["patterns"]]
-    assert names[:3] == ["contiguous", "x32_swz", "x16_swz"] and len(names) == 31
-    assert all(p["us_per_launch"] > 0 for p in out["patterns"])

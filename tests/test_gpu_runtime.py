@@ -44,6 +44,74 @@ def test_alloc_zero(rt, nbytes):
     rt.free(q)
 
 
+def test_pool_recycle_reuses_zeroed(rt):
+    # BufferPool (gpu_context.rs:31-90): recycle keeps the buffer under its 4096-aligned
+    # size, the next alloc of that size hands the same buffer out again, zeroed first.
+    rt.pool_clear()
+    p = rt.alloc(10000)
+    rt.h2d(p, np.full(10000, 0xA5, np.uint8))
+    rt.recycle(p)
+    assert rt.pool_cached_bytes() == 12288
+    with pytest.raises(t0mi.T0miError):
+        rt.recycle(p)  # no longer a live allocation
+    q = rt.alloc(12000)  # same aligned size: the pooled buffer
+    assert q == p and rt.pool_cached_bytes() == 0
+    back = np.empty(12288, np.uint8)
+    rt.d2h(q, back)
+    assert not back.any()
+    r = rt.alloc(5000)  # another size: a fresh allocation
+    assert r != q
+    rt.recycle(q)
+    rt.recycle(r)
+    assert rt.pool_cached_bytes() == 12288 + 8192
+    rt.pool_clear()
+    assert rt.pool_cached_bytes() == 0
+
+
+@pytest.mark.parametrize("n", [1, 128, 129, 1000, 4096])
+def test_alloc_f32_zeroed_padded(rt, n):
+    # alloc_f32 (gpu_context.rs:520-525): max(4n, 512) bytes rounded up to 512, zeroed,
+    # also when the pool hands back a dirty buffer of that size.
+    nbytes = (max(4 * n, 512) + 511) // 512 * 512
+    p = rt.alloc(nbytes)
+    rt.h2d(p, np.full(nbytes, 0x7F, np.uint8))
+    rt.recycle(p)
+    q = rt.alloc_f32(n)
+    back = np.empty(nbytes // 4, np.float32)
+    rt.d2h(q, back)
+    assert not back.any()
+    rt.recycle(q)
+    fresh = rt.alloc_f32(n + 5000)
+    back = np.empty(n + 5000, np.float32)
+    rt.d2h(fresh, back)
+    assert not back.any()
+    rt.free(fresh)
+    rt.pool_clear()
+
+
+def test_recycled_buffer_used_by_queued_gemm(rt):
+    # recycle does not wait: a GEMM queued on the stream that writes the buffer still runs
+    # before the buffer's next hand-out, whose zero fill comes after it in stream order.
+    m = n = k = 256
+    a = oracle.normal_bf16((m, k), 11, 0.0, 1.0)
+    b = oracle.normal_bf16((n, k), 12, 0.0, 1.0)
+    pa, pb = rt.alloc(a.nbytes), rt.alloc(b.nbytes)
+    rt.h2d(pa, a.view(np.uint16))
+    rt.h2d(pb, b.view(np.uint16))
+    py = rt.alloc_f32(m * n)
+    cfg = t0mi.auto_select_layout(m, k, n, t0mi.NT, t0mi.OUT_F32)
+    rt.gemm(cfg, pa, pb, py, m, n, k)
+    rt.recycle(py)
+    again = rt.alloc_f32(m * n)
+    assert again == py
+    back = np.empty(m * n, np.float32)
+    rt.d2h(again, back)
+    assert not back.any()
+    for p in (pa, pb, again):
+        rt.free(p)
+    rt.pool_clear()
+
+
 @pytest.mark.parametrize("offset", [0, 1, 7, 15, 16, 17])
 @pytest.mark.parametrize("size", [0, 1, 15, 16, 17, 1000, 4096 + 7, (1 << 20) + 3])
 def test_memset_any_offset_and_size(rt, offset, size):

@@ -194,3 +194,32 @@ def test_rejects_tile_without_kernel(rt):
     with pytest.raises(t0mi.T0miError) as e:
         rt.tile_gemm(t0mi.tile_preset("tile_128x128_k48").copy(tile_m=512), 0, 0, 0, 128, 128, 128)
     assert e.value.code == -2
+
+
+def _gold(name, dtype, shape):
+    import os
+    return np.fromfile(os.path.join(os.path.dirname(__file__), "golden", "torch_ref", name), dtype).reshape(shape)
+
+
+@pytest.mark.parametrize("out", ["f32", "bf16"])
+def test_torch_bf16_chain_down_projection(rt, out):
+    # precision_vs_torch.rs:115-116, 296-316: the down projection of the reference's bf16
+    # chain, swiglu_bf16_trunc [64, 512] . W_down[256, 512]^T on tile_64x64_k16 (the
+    # preset it picks for M < 128), against torch's bf16 GEMM (fixture y_bf16chain).
+    # f32 out: the reference's own bar (max|err| < 0.1), and RNE of our sum equals torch's
+    # bf16 value except at rounding boundaries; bf16 out: at most one bf16 ulp from torch.
+    m, k, n = 64, 512, 256
+    s = _gold("swiglu_bf16_trunc.bin", np.uint16, (m, k))
+    wd = _gold("w_down.bin", np.uint16, (n, k))
+    yb = _gold("y_bf16chain.bin", np.float32, (m, n))
+    dt = t0mi.OUT_BF16 if out == "bf16" else t0mi.OUT_F32
+    spec = t0mi.tile_preset("tile_64x64_k16").copy(transpose=t0mi.NT, out_dtype=dt)
+    y = run_tile(rt, spec, s, wd, m, n, k)
+    if out == "f32":
+        assert np.abs(y - yb).max() < 0.1
+        mine = oracle.bf16_to_f32(oracle.bf16_rne(y))
+    else:
+        mine = oracle.bf16_to_f32(y)
+    assert (mine == yb).mean() > 0.995
+    ulp = np.abs(yb.view(np.uint32).astype(np.int64) - mine.view(np.uint32).astype(np.int64)) >> 16
+    assert ulp.max() <= 1

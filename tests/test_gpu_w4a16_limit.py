@@ -100,3 +100,23 @@ def test_group_without_fused_kernel_refused(rt):
     tol = oracle.gemm_tolerance(k, oracle.bf16_to_f32(a), oracle.dequant_qweight_f32(w, s, z, group, 8))
     err, rel = oracle.compare(y, ref)
     assert err <= tol, (err, tol)
+
+
+@pytest.mark.parametrize("m", [100, 191])
+def test_non_pow2_group_under_limit_takes_pingpong(rt, m):
+    # group 192: a multiple of 64 but not a power of two.  With the dequant-once route ruled
+    # out, rows below the ping-pong kernel's usual threshold must still run a kernel that
+    # indexes groups by division (the ping-pong kernel), not the 128x128 fused kernel, whose
+    # k >> log2(group) would read scales and zero points of the wrong groups.
+    k, n, group = 1152, 320, 192
+    a, w, s, z = operands(m, k, n, group, 0x5500 + m)
+    (da, pa), (dw, pw), (ds, ps), (dz, pz) = [to_dev(x) for x in (a, w, s, z)]
+    dy, py = empty_dev(m * n * 4, fill=0xCD)
+    rt.set_w4a16_workspace_limit(0)
+    print(f"[w4 limit] {m}x{k}x{n} g{group} limit=0", flush=True)
+    rt.w4a16_gemm(pa, pw, ps, pz, 0, py, m, k, n, group, t0mi.OUT_F32)
+    y = from_dev(dy, np.float32, (m, n))
+    ref = oracle.w4a16_gemm(a, w, s, z, group, 8)
+    tol = oracle.gemm_tolerance(k, oracle.bf16_to_f32(a), oracle.dequant_qweight_f32(w, s, z, group, 8))
+    err, rel = oracle.compare(y, ref)
+    assert err <= tol and rel < 1e-2, (err, tol, rel)

@@ -116,6 +116,33 @@ def test_golden_torch_fixtures_bf16_rne():
     assert (trunc == bf).mean() < 0.7
 
 
+def test_golden_torch_fixtures_bf16_chain():
+    """The bf16 chain of benchmarks/gen_torch_ref.py, which precision_vs_torch.rs:115-116
+    checks its down projection against: swiglu_bf16chain = silu(h_gate_bf16acc) *
+    h_up_bf16acc in fp32; swiglu_bf16_trunc its bf16 rounding (torch's .to(bfloat16),
+    round-to-nearest-even); y_bf16chain = torch.mm of bf16 operands, bf16 output (K = 512).
+    Pins the oracle's SiLU epilogue op and RNE on these data, and the bf16-output GEMM:
+    RNE of the oracle's fp32 sum must be torch's bf16 value except at rounding
+    boundaries (torch sums in another order), and never more than one bf16 ulp away."""
+    gate = _load("h_gate_bf16acc.bin", np.float32, (64, 512))
+    up = _load("h_up_bf16acc.bin", np.float32, (64, 512))
+    chain = _load("swiglu_bf16chain.bin", np.float32, (64, 512))
+    silu = oracle.epilogue(gate, [3])  # op 3: SiLU
+    sw = (silu * up).astype(np.float32)
+    rel = np.abs(sw - chain) / np.maximum(np.abs(chain), 1e-30)
+    assert rel.max() < 1e-5, "SiLU(gate) * up, fp32"
+    assert (oracle.epilogue(gate, [2]) * up != chain).mean() > 0.5, "a ReLU in place of SiLU is caught"
+    trunc = _load("swiglu_bf16_trunc.bin", np.uint16, (64, 512))
+    assert np.array_equal(oracle.bf16_rne(chain), trunc), "torch's bf16 cast is RNE"
+    y = oracle.gemm_bf16(trunc, _load("w_down.bin", np.uint16, (256, 512)), "nt")
+    yb = _load("y_bf16chain.bin", np.float32, (64, 256))
+    mine = oracle.bf16_to_f32(oracle.bf16_rne(y))
+    assert (mine == yb).mean() > 0.995
+    ulp = np.abs(yb.view(np.uint32).astype(np.int64) - mine.view(np.uint32).astype(np.int64)) >> 16
+    assert ulp.max() <= 1
+    assert (oracle.bf16_to_f32(oracle.bf16_trunc(y)) == yb).mean() < 0.7, "truncation would be caught"
+
+
 def test_fast_loop_bit_identical_to_literal_reference_order():
     """The vectorised i-k-j loop must reproduce cpu_gemm_nt_bf16's i-j-k sequential
     fp32 order bit for bit (tile_ir.rs:5021-5038)."""
