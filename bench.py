@@ -218,6 +218,45 @@ def bench_prefill(args, torch, t0mi, rt):
     return res["default"][0], res["default"][1], res["fused"]
 
 
+SHARD_N = 1376  # config 4's N = 11008 over 8 GPUs, column-parallel
+
+
+def bench_shard(args, torch, t0mi, rt):
+    """The one-GPU stand-in for config 4's column-parallel shard over 8 GPUs: the W4A16 decode
+    GEMM 16 x 4096 x 1376 (22 strips of 64 columns; the K range split over 8 workgroups per
+    strip inside the launch), weights rotated over >= 512 MB of copies, direct launches and a
+    HIP-graph replay of the same calls."""
+    Mw, Kw, Nw, G = 16, 4096, SHARD_N, 128
+    wbytes, sbytes = Kw // 8 * Nw * 4, Kw // G * Nw * 2
+    copies = max(2, -(-512 * 1024 * 1024 // (wbytes + sbytes)))
+    g = torch.Generator(device="cuda:0")
+    g.manual_seed(0x7506)
+    a = torch.randn(Mw, Kw, device="cuda:0", generator=g).to(torch.bfloat16)
+    ws = torch.randint(-2**31, 2**31 - 1, (copies, Kw // 8, Nw), device="cuda:0", dtype=torch.int32, generator=g)
+    ss = (torch.rand(copies, Kw // G, Nw, device="cuda:0", generator=g) * 0.015 + 0.005).to(torch.bfloat16)
+    y = torch.empty(Mw, Nw, device="cuda:0", dtype=torch.bfloat16)
+    pa, py = a.data_ptr(), y.data_ptr()
+    wp = [(ws[i].data_ptr(), ss[i].data_ptr()) for i in range(copies)]
+
+    def launch_i(i):
+        pw, ps = wp[i % copies]
+        rt.w4a16_gemm(pa, pw, ps, 0, 8, py, Mw, Kw, Nw, G, t0mi.OUT_BF16)
+    warm_up(torch, lambda: launch_i(0), max(args.warmup, copies))
+    us, batches = timed_batches(torch, launch_i, max(args.steps * 4, 2 * copies))
+    gus = graph_replay_us(torch, t0mi, lambda r, i: r.w4a16_gemm(pa, wp[i % copies][0], wp[i % copies][1], 0, 8, py,
+                                                                 Mw, Kw, Nw, G, t0mi.OUT_BF16), 4 * copies)
+    alg_bytes = 2 * Mw * Kw + Kw * Nw // 2 + 2 * (Kw // G) * Nw + 2 * Mw * Nw
+    gbs = alg_bytes / (us * 1e-6) / 1e9
+    print(f"[bench] shard w4a16 decode 16x4096x{Nw} g128: {us:.2f} us/call (median of "
+          f"{', '.join(f'{b:.2f}' for b in batches)}), {gbs:.0f} GB/s; graph replay {gus} us", file=sys.stderr,
+          flush=True)
+    return {"us_per_call": round(us, 3), "value": round(gbs, 1), "unit": "GB/s", "batch_us": [round(b, 3) for b in batches],
+            "graph_replay_us_per_call": gus, "algorithmic_bytes": alg_bytes, "weight_copies_rotated": copies,
+            "workload": f"W4A16 decode A[16,4096] bf16 x int4 W[4096,{Nw}] g128 zp=8, bf16 out: config 4's "
+                        f"column-parallel shard over 8 GPUs, run on one",
+            "roofline": roofline("hbm", gbs, load_traffic("w4a16_shard"))}
+
+
 def bench_w4a16(args, torch, t0mi, rt):
     Mw, Kw, Nw, G = args.rows, 4096, 11008, 128
     wbytes = Kw // 8 * Nw * 4
@@ -339,8 +378,9 @@ def cpu_model() -> str:
 
 def cpu_baseline(which, budget_s: float = 10.0):
     """The oracle (C restatement of cpu_gemm_nt_bf16 -- one fp32 accumulator per output, k
-    ascending -- with OpenMP over output rows) timed on this host's cores for about budget_s
-    seconds of CPU work, plus a one-core rate from a 64-row sample."""
+    ascending -- with OpenMP over output rows; for W4A16 the exact fp32 dequant first) timed
+    on this host's cores for about budget_s seconds of CPU work (at least one full call),
+    on the same shape as the GPU leg; the 4096^3 leg adds a one-core rate from 64 rows."""
     import numpy as np  # noqa: F401
     import oracle  # the CPU baseline leg is the only bench code that uses the oracle
     threads = oracle.num_threads()
@@ -355,30 +395,51 @@ def cpu_baseline(which, budget_s: float = 10.0):
             if time.perf_counter() - t0 > budget_s:
                 return (time.perf_counter() - t0) / reps, reps
 
+    def gemm_leg(M, N, K, sd, seed, what):
+        a = oracle.normal_bf16((M, K), seed, 0.0, sd)
+        b = oracle.normal_bf16((K, N), seed + 1, 0.0, sd)
+        dt, reps = timed(lambda: oracle.gemm_bf16(a, b, "nn"))
+        return dt, reps, {"sample": f"full {what} NN GEMM x{reps} ({dt:.3f} s each) with OpenMP over rows; "
+                                    f"sequential fp32 per output as cpu_gemm_nt_bf16 (src/t0/tile_ir.rs:5021-5038)"}
+
+    def w4_leg(M, K, N, G, zeros, what):
+        a = oracle.normal_bf16((M, K), 1, 0.0, 1.0)
+        w = oracle.pack_qweight(oracle.nibbles((K, N), 2))
+        s = oracle.uniform_bf16((K // G, N), 3, 0.005, 0.02)
+        z = oracle.pack_qzeros(oracle.nibbles((K // G, N), 4)) if zeros else None
+        dt, reps = timed(lambda: oracle.w4a16_gemm(a, w, s, z, G, 8))
+        return dt, reps, {"sample": f"full {what} GEMM x{reps} ({dt * 1e3:.0f} ms each): exact fp32 dequant "
+                                    f"((q - z) * s, quant_kernels.rs:24) then the sequential-fp32 loop, OpenMP over rows"}
+
+    base = {"cores": threads, "kind": "port", "cpu_model": model}
     if which == "gemm":
         M = N = K = 4096
-        a = oracle.normal_bf16((M, K), 0x7501, 0.0, 1.0)
+        dt, reps, info = gemm_leg(M, N, K, 1.0, 0x7501, "4096^3")
+        a = oracle.normal_bf16((64, K), 0x7501, 0.0, 1.0)
         b = oracle.normal_bf16((K, N), 0x7502, 0.0, 1.0)
-        dt, reps = timed(lambda: oracle.gemm_bf16(a, b, "nn"))
         t1 = time.perf_counter()
-        oracle.gemm_bf16(a[:64], b, "nn", nthreads=1)
+        oracle.gemm_bf16(a, b, "nn", nthreads=1)
         one = 2.0 * 64 * N * K / (time.perf_counter() - t1) / 1e12
-        return {"value": round(2.0 * M * N * K / dt / 1e12, 4), "unit": "TFLOPS", "cores": threads, "kind": "port",
-                "cpu_model": model,
-                "one_core_TFLOPS": round(one, 5),
-                "sample": f"full 4096^3 NN GEMM x{reps} ({dt:.2f} s each) with OpenMP over rows; one-core rate "
-                          f"from 64 rows; sequential fp32 per output as cpu_gemm_nt_bf16 "
-                          f"(src/t0/tile_ir.rs:5021-5038)"}
-    Mw, Kw, Nw, G = 16, 4096, 11008, 128
-    a = oracle.normal_bf16((Mw, Kw), 1, 0.0, 1.0)
-    w = oracle.pack_qweight(oracle.nibbles((Kw, Nw), 2))
-    s = oracle.uniform_bf16((Kw // G, Nw), 3, 0.005, 0.02)
-    dt, reps = timed(lambda: oracle.w4a16_gemm(a, w, s, None, G, 8))
+        return {"value": round(2.0 * M * N * K / dt / 1e12, 4), "unit": "TFLOPS", **base,
+                "one_core_TFLOPS": round(one, 5), **info}
+    if which == "skinny":
+        M, N, K = 128, 4096, 4096
+        dt, reps, info = gemm_leg(M, N, K, 0.02, 0x7503, "128x4096x4096")
+        return {"value": round((2 * M * K + 2 * K * N + 2 * M * N) / dt / 1e9, 3), "unit": "GB/s", **base, **info}
+    if which == "prefill":
+        M, K, N, G = 4096, 4096, 14336, 128
+        dt, reps, info = w4_leg(M, K, N, G, True, "4096x4096x14336 g128 W4A16 prefill")
+        return {"value": round(2.0 * M * N * K / dt / 1e12, 4), "unit": "TFLOPS", **base, **info}
+    Mw, Kw, Nw, G = 16, 4096, (1376 if which == "shard" else 11008), 128
+    dt, reps, info = w4_leg(Mw, Kw, Nw, G, False, f"16x4096x{Nw} decode")
     alg_bytes = 2 * Mw * Kw + Kw * Nw // 2 + 2 * (Kw // G) * Nw + 2 * Mw * Nw
-    return {"value": round(alg_bytes / dt / 1e9, 3), "unit": "GB/s", "cores": threads, "kind": "port",
-            "cpu_model": model,
-            "sample": f"full 16x4096x11008 decode GEMM x{reps} ({dt*1e3:.0f} ms each): exact fp32 dequant "
-                      f"then the sequential-fp32 loop, OpenMP over rows"}
+    return {"value": round(alg_bytes / dt / 1e9, 3), "unit": "GB/s", **base, **info}
+
+
+def roofline(bound, achieved, traffic):
+    peak = PEAK_HBM_GBS if bound == "hbm" else PEAK_BF16_TFLOPS
+    return {"bound": bound, "achieved": round(achieved, 2), "peak": peak, "unit": "GB/s" if bound == "hbm" else "TFLOP/s",
+            "frac": round(achieved / peak, 4), "traffic": traffic}
 
 
 def copy_calibration(args, torch):
@@ -637,52 +698,32 @@ def main():
     rt = t0mi.Runtime.on_torch_stream(0)
     out = {"metric": METRIC, "n_gpus": 1, "steps": args.steps, "warmup": args.warmup, "higher_is_better": True,
            "scaling": "weak", "vs_baseline": None, "dtype": "bf16", "data": "synthetic"}
-    if args.only == "skinny":
-        cfg, us, gbs, alg_bytes, tuned = bench_skinny(args, torch, t0mi, rt)
-        out.update({"metric": "skinny bf16 GEMM HBM GB/s (% peak)", "value": round(gbs, 1), "unit": "GB/s",
-                    "ms_per_step": round(us * 1e-3, 6),
-                    "config": {"workload": "bf16 GEMM M=128, N=4096, K=4096 NN, N(0,0.02), bf16 out "
-                                           "(BASELINE config 3); one call = GEMM + split-K reduce",
-                               "kernel": cfg.name()},
-                    "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
-                                 "frac": round(gbs / PEAK_HBM_GBS, 4), "traffic": load_traffic("gemm_skinny")}})
-        if tuned:
-            out["tuned"] = tuned
-        rt.close()
-        print(json.dumps(out), flush=True)
-        return
-    if args.only == "prefill":
-        us, tflops, (fus_us, fus_tf) = bench_prefill(args, torch, t0mi, rt)
-        out.update({"metric": "W4A16 prefill TFLOPS (% MFMA peak)", "value": round(tflops, 2), "unit": "TFLOPS",
-                    "fused_route": {"us": round(fus_us, 2), "TFLOPS": round(fus_tf, 2),
-                                    "frac": round(fus_tf / PEAK_BF16_TFLOPS, 4),
-                                    "how": "t0mi_set_w4a16_workspace_limit(ctx, 0): dequant inside the K loop",
-                                    "traffic": (load_traffic("w4a16_prefill_fused_detail") or {}).get("call_bytes")},
-                    "ms_per_step": round(us * 1e-3, 6),
-                    "config": {"workload": "W4A16 A[4096,4096] bf16 x int4 W[4096,14336] g128, per-group zero "
-                                           "points, bf16 out (BASELINE config 5); one call = t0mi_w4a16_gemm"},
-                    "roofline": {"bound": "mfma", "achieved": round(tflops, 2), "peak": PEAK_BF16_TFLOPS,
-                                 "unit": "TFLOP/s", "frac": round(tflops / PEAK_BF16_TFLOPS, 4),
-                                 "traffic": load_traffic("w4a16_prefill")}})
-        rt.close()
-        print(json.dumps(out), flush=True)
-        return
-    if args.only in ("all", "gemm"):
+    legs = ("gemm", "w4a16", "skinny", "prefill", "shard") if args.only == "all" else (args.only,)
+    cpu = {}
+
+    def baseline(which):
+        if args.no_cpu:
+            return None
+        try:
+            return cpu_baseline(which, budget_s=10.0 if which in ("gemm", "w4a16") else 5.0)
+        except Exception as e:  # the baseline is reported, never required
+            return {"value": None, "error": str(e)}
+
+    if "gemm" in legs:
         cfg, ms, tflops, batches = bench_gemm(args, torch, t0mi, rt)
         out.update({"value": round(tflops, 2), "unit": "TFLOPS", "ms_per_step": round(ms, 5),
                     "timing": f"median of {len(batches)} batches of {args.steps} launches (HIP events)",
                     "batch_us": [round(b, 2) for b in batches],
                     "config": {"workload": "bf16 GEMM M=N=K=4096, A[M,K] x B[K,N] row-major (NN), N(0,1), "
                                            "fp32 accumulate, bf16 out (BASELINE config 2)",
-                               "M": 4096, "N": 4096, "K": 4096, "kernel": cfg.name()}})
+                               "M": 4096, "N": 4096, "K": 4096, "kernel": cfg.name()},
+                    "roofline": roofline("mfma", tflops, load_traffic("gemm_4096"))})
         if args.tuned:
             out["tuned"] = args.tuned
         if args.gemm_clocks:
             out["clocks_during_sustained_launches"] = args.gemm_clocks
-        traffic = load_traffic("gemm_4096")
-        out["roofline"] = {"bound": "mfma", "achieved": round(tflops, 2), "peak": PEAK_BF16_TFLOPS,
-                           "unit": "TFLOP/s", "frac": round(tflops / PEAK_BF16_TFLOPS, 4), "traffic": traffic}
-    if args.only in ("all", "w4a16"):
+        cpu["gemm"] = baseline("gemm")
+    if "w4a16" in legs:
         us, gbs, alg_bytes, copies, wb = bench_w4a16(args, torch, t0mi, rt)
         w = {"value": round(gbs, 1), "unit": "GB/s", "us_per_call": round(us, 3),
              "batch_us": [round(b, 3) for b in wb],
@@ -693,24 +734,66 @@ def main():
              "workload": f"W4A16 decode A[{args.rows},4096] bf16 x int4 W[4096,11008] g128 zp=8, bf16 out"
                          + (" (BASELINE config 4)" if args.rows == 16 else "")}
         out["w4a16_decode"] = w
-        out["roofline_w4a16"] = {"bound": "hbm", "achieved": round(gbs, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
-                                 "frac": round(gbs / PEAK_HBM_GBS, 4),
-                                 "traffic": load_traffic("w4a16_decode") if args.rows == 16 else None}
-        if args.only == "w4a16":
-            out.update({"value": round(gbs, 1), "unit": "GB/s", "ms_per_step": round(us * 1e-3, 6),
-                        "config": {"workload": w["workload"]}})
-            out["roofline"] = out.pop("roofline_w4a16")
-    if not args.no_cpu:
-        try:
-            if args.only in ("all", "gemm"):
-                out["cpu_baseline"] = cpu_baseline("gemm")
-            if args.only in ("all", "w4a16"):
-                out["cpu_baseline_w4a16"] = cpu_baseline("w4a16")
-            if args.only == "w4a16":
-                out["cpu_baseline"] = out.pop("cpu_baseline_w4a16")
-        except Exception as e:  # the baseline is reported, never required
-            out["cpu_baseline"] = {"value": None, "error": str(e)}
+        out["roofline_w4a16"] = roofline("hbm", gbs, load_traffic("w4a16_decode") if args.rows == 16 else None)
+        cpu["w4a16"] = baseline("w4a16")
+    if "skinny" in legs:
+        cfg, us, gbs, alg_bytes, tuned = bench_skinny(args, torch, t0mi, rt)
+        out["skinny"] = {"value": round(gbs, 1), "unit": "GB/s", "us_per_call": round(us, 3),
+                         "algorithmic_bytes": alg_bytes, "kernel": cfg.name(),
+                         "workload": "bf16 GEMM M=128, N=4096, K=4096 NN, N(0,0.02), bf16 out (BASELINE config 3), "
+                                     "B rotated over 16 copies",
+                         "roofline": roofline("hbm", gbs, load_traffic("gemm_skinny"))}
+        if tuned:
+            out["skinny"]["tuned"] = tuned
+        cpu["skinny"] = baseline("skinny")
+    if "prefill" in legs:
+        us, tflops, (fus_us, fus_tf) = bench_prefill(args, torch, t0mi, rt)
+        work = ("W4A16 A[4096,4096] bf16 x int4 W[4096,14336] g128, per-group zero points, bf16 out "
+                "(BASELINE config 5); one call = t0mi_w4a16_gemm")
+        out["prefill"] = {"value": round(tflops, 2), "unit": "TFLOPS", "us_per_call": round(us, 2), "workload": work,
+                          "route": "default (t0mi_w4a16_gemm as called)",
+                          "roofline": roofline("mfma", tflops, load_traffic("w4a16_prefill"))}
+        out["prefill_fused"] = {"value": round(fus_tf, 2), "unit": "TFLOPS", "us_per_call": round(fus_us, 2),
+                                "workload": work,
+                                "route": "t0mi_set_w4a16_workspace_limit(ctx, 0): dequant inside the MFMA K loop",
+                                "roofline": roofline("mfma", fus_tf, (load_traffic("w4a16_prefill_fused_detail")
+                                                                      or {}).get("call_bytes"))}
+        cpu["prefill"] = baseline("prefill")
+    if "shard" in legs:
+        out["shard"] = bench_shard(args, torch, t0mi, rt)
+        cpu["shard"] = baseline("shard")
     rt.close()
+    if args.only != "all":
+        # One leg alone: its figures are the line's own.
+        leg = {"gemm": None, "w4a16": "w4a16_decode", "skinny": "skinny", "prefill": "prefill", "shard": "shard"}
+        key = leg.get(args.only)
+        if key:
+            o = out.pop(key)
+            out["metric"] = {"w4a16_decode": "W4A16 decode HBM GB/s (% peak)", "skinny": "skinny bf16 GEMM HBM GB/s (% peak)",
+                             "prefill": "W4A16 prefill TFLOPS (% MFMA peak)",
+                             "shard": "W4A16 decode shard HBM GB/s (% peak)"}[key]
+            us = o.get("us_per_call")
+            out.update({"value": o["value"], "unit": o["unit"], "ms_per_step": round(us * 1e-3, 6),
+                        "config": {"workload": o["workload"], **({"kernel": o["kernel"]} if "kernel" in o else {})},
+                        "roofline": out.pop("roofline_w4a16") if key == "w4a16_decode" else o.pop("roofline")})
+            if key == "prefill":
+                out["fused_route"] = out.pop("prefill_fused")
+            out[key + "_detail"] = o
+        c = cpu.get(args.only)
+        if c:
+            out["cpu_baseline"] = c
+    else:
+        if cpu.get("gemm"):
+            out["cpu_baseline"] = cpu["gemm"]
+        for key, leg in (("w4a16", "cpu_baseline_w4a16"), ("skinny", "skinny"), ("prefill", "prefill"),
+                         ("shard", "shard")):
+            c = cpu.get(key)
+            if not c:
+                continue
+            if key == "w4a16":
+                out[leg] = c
+            else:
+                out[leg]["cpu_baseline"] = c
     print(json.dumps(out), flush=True)
 
 

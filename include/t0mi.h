@@ -267,6 +267,16 @@ int t0mi_gemm(t0mi_ctx* ctx, const t0mi_gemm_config* cfg, uint64_t x, uint64_t b
 int t0mi_gemm_noalloc(t0mi_ctx* ctx, const t0mi_gemm_config* cfg, uint64_t x, uint64_t b, uint64_t y,
                       uint64_t bias, uint32_t m, uint32_t n, uint32_t k);
 
+/* No counterpart in the reference (RDNA parts have one L2).  The XCD count of
+ * this runtime's device when the in-launch split-K exchange is on (workgroup i
+ * of a launch was found on XCD i % n for every i by a probe at runtime
+ * creation), or 0 when it is off and the kernels that use it fall back to
+ * split-K planes summed by a second launch; and, when `misplaced` is not null,
+ * whether any exchange launch on this runtime found one of its workgroups on
+ * another XCD than planned (its result would then be wrong; waits for the
+ * stream).  For tests and callers that check what runs. */
+int t0mi_xcd_placement(t0mi_ctx* ctx, uint32_t* n_xcd, uint32_t* misplaced);
+
 /* ---- batched submission: DispatchQueue (src/t0/prefill_dispatch.rs:58-214) - */
 typedef struct t0mi_dispatch_queue t0mi_dispatch_queue;
 /* DispatchQueue::new (prefill_dispatch.rs:73-79). */

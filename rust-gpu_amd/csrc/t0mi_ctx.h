@@ -13,6 +13,10 @@
 #include "t0mi_internal.h"
 
 namespace t0mi {
+struct XcdExchange;  // xcd_exchange.h
+}
+
+namespace t0mi {
 
 typedef void (*GemmLaunchFn)(dim3 grid, hipStream_t stream, const GemmParams& p);
 struct GemmLaunchEntry {
@@ -88,6 +92,15 @@ struct t0mi_ctx {
   uint32_t last_grid[3] = {0, 0, 0};
   std::vector<uint8_t> last_ka;
   int cu_count = 256;
+  // In-launch split-K exchange through one XCD's L2 (xcd_exchange.h): the XCD
+  // count when the placement probe found workgroup i on XCD i % xk_nx for every
+  // i (0: the probe failed; kernels then keep their split-K planes), the
+  // counters (xk_nx groups of kXkCountersPerXcd, zeroed once, left zeroed by
+  // every launch), the misplacement flag after them, and the partial slots.
+  uint32_t xk_nx = 0;
+  uint32_t* xk_tick = nullptr;
+  void* xk_part = nullptr;
+  size_t xk_part_bytes = 0;
 };
 
 // Scoped hold of ctx->submit_mu (ctx must be non-null).
@@ -98,6 +111,17 @@ namespace t0mi {
 int ensure_workspace(t0mi_ctx* ctx, size_t bytes);
 // Grows ctx->cvt to at least `bytes` (waits for the stream first).
 int ensure_cvt_buffer(t0mi_ctx* ctx, size_t bytes);
+// Counters of the XCD exchange, per XCD: at most this many tiles per XCD per launch.
+// Each counter has a 256-byte slot of its own: atomics on one line (or one L2
+// channel) are serialized, and a launch's pieces all arrive at about the same
+// time (176 tickets on one line: 19 us for a 8 us decode).
+constexpr uint32_t kXkCountersPerXcd = 1024;
+constexpr uint32_t kXkCounterStride = 64;  // u32s between counters
+// Readies the XCD exchange for a launch of `tiles` tiles with `part_bytes` of
+// partial slots: false (no error set) when the device's placement did not
+// check out or the tiles do not fit the counters; T0MI_ERR_* when a buffer
+// could not be made.  Fills *x.
+int xk_prepare(t0mi_ctx* ctx, uint32_t tiles, size_t part_bytes, XcdExchange* x, bool* ok);
 // Runs a GEMM with the best prebuilt config for (m, n, k, transpose) and the
 // given output type (cost-model ranking, as t0mi_auto_select), as two launches
 // over column ranges where plan_column_split says so.  Asynchronous.

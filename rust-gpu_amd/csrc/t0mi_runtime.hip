@@ -16,6 +16,7 @@
 #include <time.h>
 
 #include "t0mi_ctx.h"
+#include "xcd_exchange.h"
 
 using namespace t0mi;
 
@@ -138,6 +139,41 @@ int ensure_cvt_buffer(t0mi_ctx* ctx, size_t bytes) {
   e = hipMalloc(&ctx->cvt, want);
   if (e != hipSuccess) return hip_fail(e, "hipMalloc(conversion buffer)");
   ctx->cvt_bytes = want;
+  return T0MI_OK;
+}
+
+int xk_prepare(t0mi_ctx* ctx, uint32_t tiles, size_t part_bytes, XcdExchange* x, bool* ok) {
+  *ok = false;
+  if (ctx->null_backend || ctx->xk_nx == 0) return T0MI_OK;
+  if ((tiles + ctx->xk_nx - 1) / ctx->xk_nx > kXkCountersPerXcd) return T0MI_OK;
+  const size_t tick_bytes = ((size_t)ctx->xk_nx * kXkCountersPerXcd + 1) * kXkCounterStride * 4;  // + the flag
+  if (!ctx->xk_tick) {
+    if (int rc = check_growth(ctx, "the exchange counters", 0, tick_bytes)) return rc;
+    hipError_t e = hipMalloc((void**)&ctx->xk_tick, tick_bytes);
+    if (e != hipSuccess) return hip_fail(e, "hipMalloc(exchange counters)");
+    if (int rc = fill_async(ctx, ctx->xk_tick, 0, tick_bytes)) return rc;
+    e = hipStreamSynchronize(ctx->stream);
+    if (e != hipSuccess) return hip_fail(e, "hipStreamSynchronize");
+  }
+  if (ctx->xk_part_bytes < part_bytes) {
+    if (int rc = check_growth(ctx, "the exchange slots", ctx->xk_part_bytes, part_bytes)) return rc;
+    hipError_t e = hipStreamSynchronize(ctx->stream);
+    if (e != hipSuccess) return hip_fail(e, "hipStreamSynchronize");
+    if (ctx->xk_part) (void)hipFree(ctx->xk_part);
+    ctx->xk_part = nullptr;
+    ctx->xk_part_bytes = 0;
+    const size_t want = part_bytes + (part_bytes >> 2);
+    e = hipMalloc(&ctx->xk_part, want);
+    if (e != hipSuccess) return hip_fail(e, "hipMalloc(exchange slots)");
+    ctx->xk_part_bytes = want;
+  }
+  x->part = (float*)ctx->xk_part;
+  x->tick = ctx->xk_tick;
+  x->flag = ctx->xk_tick + (size_t)ctx->xk_nx * kXkCountersPerXcd * kXkCounterStride;
+  x->nx = ctx->xk_nx;
+  x->tpx = kXkCountersPerXcd;
+  x->stride = kXkCounterStride;
+  *ok = true;
   return T0MI_OK;
 }
 
@@ -302,6 +338,62 @@ static int scratch_for_device(int dev, void** out) {
   return T0MI_OK;
 }
 
+// ------------------------------------------------ XCD placement probe ----
+
+// Workgroup i records the XCD it runs on.
+__global__ void t0mi_placement_kernel(uint32_t* out) {
+  if (threadIdx.x == 0) out[blockIdx.x] = t0mi::xcc_id();
+}
+
+// Once per device (the caller has made it current): launches the probe at
+// several grid sizes and returns nx when every workgroup i of every launch ran
+// on XCD i % nx (nx = the number of XCDs seen), else 0.  The in-launch
+// exchange of split-K partials relies on it.
+static uint32_t placement_for_device(int dev) {
+  static std::mutex mu;
+  static std::map<int, uint32_t> known;
+  std::lock_guard<std::mutex> lock(mu);
+  auto it = known.find(dev);
+  if (it != known.end()) return it->second;
+  uint32_t nx = 0;
+  constexpr uint32_t kMaxGrid = 4096;
+  uint32_t* d = nullptr;
+  hipStream_t st = nullptr;
+  std::vector<uint32_t> h(kMaxGrid);
+  bool ok = hipMalloc((void**)&d, kMaxGrid * 4) == hipSuccess &&
+            hipStreamCreateWithFlags(&st, hipStreamNonBlocking) == hipSuccess;
+  for (uint32_t grid : {64u, 1000u, kMaxGrid}) {
+    if (!ok) break;
+    hipLaunchKernelGGL(t0mi_placement_kernel, dim3(grid), dim3(64), 0, st, d);
+    ok = hipGetLastError() == hipSuccess && hipMemcpyAsync(h.data(), d, grid * 4, hipMemcpyDeviceToHost, st) == hipSuccess &&
+         hipStreamSynchronize(st) == hipSuccess;
+    if (!ok) break;
+    uint32_t seen = 0;
+    for (uint32_t i = 0; i < grid; ++i) seen = std::max(seen, h[i] + 1);
+    for (uint32_t i = 0; i < grid && ok; ++i) ok = h[i] == i % seen;
+    if (ok && nx && seen != nx) ok = false;
+    nx = seen;
+  }
+  if (st) (void)hipStreamDestroy(st);
+  if (d) (void)hipFree(d);
+  (void)hipGetLastError();  // a failed probe only turns the exchange off
+  const uint32_t res = ok && nx >= 1 && nx <= 16 ? nx : 0;
+  known.emplace(dev, res);
+  return res;
+}
+
+extern "C" int t0mi_xcd_placement(t0mi_ctx* ctx, uint32_t* n_xcd, uint32_t* misplaced) {
+  if (!ctx) return set_error(T0MI_ERR_INVALID, "null runtime");
+  if (n_xcd) *n_xcd = ctx->xk_nx;
+  if (misplaced) *misplaced = 0;
+  if (ctx->null_backend || !ctx->xk_tick || !misplaced) return T0MI_OK;
+  if (int rc = refuse_if_capturing(ctx, "t0mi_xcd_placement")) return rc;
+  hipError_t e = hipMemcpyAsync(misplaced, ctx->xk_tick + (size_t)ctx->xk_nx * kXkCountersPerXcd * kXkCounterStride, 4,
+                                hipMemcpyDeviceToHost, ctx->stream);
+  if (e == hipSuccess) e = hipStreamSynchronize(ctx->stream);
+  return e == hipSuccess ? T0MI_OK : hip_fail(e, "reading the placement flag");
+}
+
 // ===================================================================== C ABI ==
 
 static int ctx_create(int device, bool use_given_stream, void* hip_stream, t0mi_ctx** out) {
@@ -346,6 +438,7 @@ static int ctx_create(int device, bool use_given_stream, void* hip_stream, t0mi_
   }
   // A failed lookup leaves the runtime usable; only t0mi_gemm_noalloc reports it.
   c->scratch_rc = scratch_for_device(dev, &c->scratch);
+  c->xk_nx = placement_for_device(dev);
   *out = c;
   return T0MI_OK;
 }
@@ -374,6 +467,8 @@ extern "C" void t0mi_ctx_destroy(t0mi_ctx* ctx) {
       for (uint64_t p : kv.second) (void)hipFree((void*)p);
     if (ctx->ws) (void)hipFree(ctx->ws);
     if (ctx->cvt) (void)hipFree(ctx->cvt);
+    if (ctx->xk_tick) (void)hipFree(ctx->xk_tick);
+    if (ctx->xk_part) (void)hipFree(ctx->xk_part);
     if (ctx->own_stream) (void)hipStreamDestroy(ctx->stream);
   }
   delete ctx;

@@ -361,6 +361,7 @@ static constexpr uint32_t kPingPongRows = 192;
 static constexpr uint32_t kTwoPassRows = 1536;
 static constexpr uint32_t kSplitRouteRows = 1024;
 static constexpr uint32_t kPrefillTwoPassRows = 768;  // groups or K the ping-pong kernel does not take
+static constexpr uint32_t kXkMaxPieces = 16;          // pieces per strip the decode kernel's sum takes
 
 static int launch_dequant(t0mi_ctx* ctx, uint64_t qweight, uint64_t scales, uint64_t qzeros, uint32_t zp_const,
                           uint64_t out, uint32_t k, uint32_t n, uint32_t group, uint32_t round_mode) {
@@ -424,6 +425,81 @@ static int launch_w4_pingpong(t0mi_ctx* ctx, uint64_t a, uint64_t qweight, uint6
   if (e != hipSuccess) return hip_fail(e, "w4a16 ping-pong launch");
   if (sk > 1) return launch_splitk_reduce(ctx, (const float*)ctx->ws, (void*)y, nullptr, m, n, n, sk, out_bf16, EpiChain{});
   return T0MI_OK;
+}
+
+// One slab (m <= 16), groups 32..256, when N has too few 64-column strips to
+// give every CU one (strips * 2 <= CUs): the decode kernel with its K range
+// split over workgroups inside one launch (w4a16_decode_v2 with XK).  The
+// pieces of a strip are combined in the strip's XCD's L2 by the last piece to
+// arrive.  The largest power-of-two piece count up to 8 that keeps strips *
+// pieces <= CUs; a piece is nw waves of kbw k-blocks (whole groups).
+// Measured at K = 4096, group 128 (per call, against one workgroup per strip):
+// N = 1376 (the column-parallel shard of config 4 over 8 GPUs): 8 pieces of
+// 4 waves x 4 k-blocks, 4.90 against 7.36 us; N = 2752: 4 pieces of 8 x 4, 5.55
+// against 7.25 us; N = 5504: 2 pieces of 8 x 8, 6.88 against 7.36 us; N = 11008
+// (config 4): every split measured slower (9.3-10.8 us against 8.1: the
+// exchange's store, ticket and slot reads cost ~2 us under full HBM load), so
+// wide N keeps one workgroup per strip.  Returns 1 when the split does not
+// apply (the caller takes the strip-per-workgroup route).
+static int launch_decode_xk(t0mi_ctx* ctx, W4Params p, uint32_t m, uint32_t k, uint32_t n, uint32_t group,
+                            uint64_t y, bool zeros) {
+  const uint32_t kbpg = group / 32, kb_tot = k / 32, strips = (n + 63) / 64, unit = std::max(4u, kbpg);
+  const uint32_t cus = (uint32_t)ctx->cu_count;
+  uint32_t pieces = 8;
+  while (pieces > 1 && strips * pieces > cus) pieces /= 2;
+  if (pieces == 1 || kb_tot < 2 * unit) return 1;
+  // k-blocks of a piece, then 4 waves for up to 16 of them, else 8, each wave
+  // a whole number of groups (at most 16 k-blocks: the registers of 16 loads).
+  const uint32_t kbr = (kb_tot + pieces - 1) / pieces;
+  const uint32_t nw = kbr <= 16 ? 4 : 8;
+  const uint32_t kbw = ((kbr + nw - 1) / nw + unit - 1) / unit * unit;
+  if (kbw > 16) return 1;
+  pieces = (kb_tot + nw * kbw - 1) / (nw * kbw);
+  if (pieces < 2 || pieces > kXkMaxPieces) return 1;
+  XcdExchange x;
+  bool ok = false;
+  int rc = xk_prepare(ctx, strips, (size_t)strips * pieces * 1024 * 4, &x, &ok);
+  if (rc) return rc;
+  if (!ok) return 1;
+  p.M = m;
+  p.y = (void*)y;
+  p.strips = strips;
+  p.pieces = pieces;
+  p.xk = x;
+  const uint32_t grid = (strips + x.nx - 1) / x.nx * x.nx * pieces;
+  // CH: chunks of 4 k-blocks (whole groups for group 256).
+#define T0MI_XK(NW, KBW, G)                                                                                        \
+  if (zeros)                                                                                                      \
+    hipLaunchKernelGGL((w4a16_decode_v2<NW, KBW, G / 32, true, KBW / (G / 32 > 4 ? G / 32 : 4), 1, true>),      \
+                       dim3(grid), dim3(NW * 64), 0, ctx->stream, p);                                             \
+  else                                                                                                            \
+    hipLaunchKernelGGL((w4a16_decode_v2<NW, KBW, G / 32, false, KBW / (G / 32 > 4 ? G / 32 : 4), 1, true>),     \
+                       dim3(grid), dim3(NW * 64), 0, ctx->stream, p);
+#define T0MI_XK_W(NW, G)              \
+  if (kbw == 4) {                     \
+    T0MI_XK(NW, (G == 256 ? 8 : 4), G) \
+  } else if (kbw == 8) {              \
+    T0MI_XK(NW, 8, G)                 \
+  } else {                            \
+    T0MI_XK(NW, 16, G)                \
+  }
+#define T0MI_XK_G(NW)                   \
+  switch (group) {                      \
+    case 32: T0MI_XK_W(NW, 32) break;   \
+    case 64: T0MI_XK_W(NW, 64) break;   \
+    case 128: T0MI_XK_W(NW, 128) break; \
+    default: T0MI_XK_W(NW, 256) break;  \
+  }
+  if (nw == 4) {
+    T0MI_XK_G(4)
+  } else {
+    T0MI_XK_G(8)
+  }
+#undef T0MI_XK_G
+#undef T0MI_XK_W
+#undef T0MI_XK
+  hipError_t e = hipGetLastError();
+  return e == hipSuccess ? T0MI_OK : hip_fail(e, "w4a16 decode launch");
 }
 
 extern "C" int t0mi_set_w4a16_workspace_limit(t0mi_ctx* ctx, uint64_t bytes) {
@@ -575,6 +651,10 @@ extern "C" int t0mi_w4a16_gemm(t0mi_ctx* ctx, uint64_t a, uint64_t qweight, uint
   // workgroups of 16 k-blocks per wave, issued and computed in chunks of one
   // group or 4 blocks), other groups the generic kernel.
   const bool v2 = group == 32 || group == 64 || group == 128 || group == 256;
+  if (v2 && m <= 16) {
+    rc = launch_decode_xk(ctx, p, m, k, n, group, y, qzeros != 0);
+    if (rc <= 0) return rc;  // launched, or failed; 1: the exchange is off, take the planes route
+  }
   constexpr int KBW2 = 16;
   constexpr int WAVES = 8, KBW = 16;  // generic kernel
   const uint32_t kb_tot = k / 32;

@@ -26,6 +26,7 @@
 // as 8-byte bf16 (16-byte f32) row segments.
 #pragma once
 #include "gemm_bf16_kernel.h"
+#include "xcd_exchange.h"
 
 namespace t0mi {
 
@@ -44,6 +45,10 @@ struct W4Params {
   uint64_t y_split_stride; // bytes between partial planes when gridDim.y > 1
   uint32_t nib_mask;       // 0x000F000F (see nib_pairs_ao)
   uint32_t nib_magic;      // 0x43004300
+  // In-launch K split (w4a16_decode_v2 with XK): 64-column strips, K pieces per
+  // strip (pieces * NW * KBW k-blocks cover K), and the XCD exchange.
+  uint32_t strips, pieces;
+  XcdExchange xk;
 };
 
 __device__ __forceinline__ bf16x8_t nib_pairs(uint32_t w) {
@@ -95,10 +100,18 @@ __device__ __forceinline__ float bf16f(uint32_t h) { return __builtin_bit_cast(f
 // RS row slabs of 16 (1..4) share one pass over the weights: each dequantized
 // weight fragment feeds every slab's MFMAs, and every row goes through exactly
 // the operations of a 16-row launch on its own slab (bit-identical results).
-template <int NW, int KBW, int KBPG, bool ZEROS, int CH = 1, int RS = 1>
+//
+// XK (one slab): a 1-D grid of strips x p.pieces workgroups numbered for the
+// XCD exchange (xcd_exchange.h); piece c of a strip covers k-blocks
+// [c * NW * KBW, (c + 1) * NW * KBW).  With one piece the strip is stored
+// directly; otherwise the pieces' [16 x 64] fp32 partials meet in the strip's
+// XCD's L2 and the last piece sums them in piece order and stores Y, all in
+// this launch: every CU gets several workgroups however few strips N has.
+template <int NW, int KBW, int KBPG, bool ZEROS, int CH = 1, int RS = 1, bool XK = false>
 __global__ __launch_bounds__(NW * 64) void w4a16_decode_v2(W4Params p) {
   static_assert(KBW % KBPG == 0, "whole groups per wave");
   static_assert(RS >= 1 && RS <= 4, "one to four row slabs");
+  static_assert(!XK || RS == 1, "the in-launch K split runs one slab");
   // CH chunks per wave: chunk c's loads are issued, then its blocks computed,
   // before chunk c+1's loads (CB blocks, whole groups and pairs per chunk).
   constexpr int CB = KBW / CH;
@@ -107,12 +120,18 @@ __global__ __launch_bounds__(NW * 64) void w4a16_decode_v2(W4Params p) {
   // addresses are scalar arithmetic (3 % faster than as a per-lane value).
   const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
   const int c = lane & 15, g = lane >> 4;
-  const int n0 = blockIdx.x * 64;
+  uint32_t strip = blockIdx.x, part = blockIdx.y;
+  if (XK) {
+    xk_unpack(blockIdx.x, p.xk.nx, p.pieces, &strip, &part);
+    if (strip >= p.strips) return;  // the numbering's padding (whole workgroup)
+    xk_check_placement(p.xk);
+  }
+  const int n0 = (int)strip * 64;
   const int ncol = n0 + 4 * c;
   const bool col_ok = ncol < (int)p.N;  // N % 8 == 0, so the whole quad is in range
   const int ncol_c = col_ok ? ncol : 0;
   const int kb_tot = (int)(p.K / 32);
-  const int kb0 = __builtin_amdgcn_readfirstlane(((int)blockIdx.y * NW + wave) * KBW);
+  const int kb0 = __builtin_amdgcn_readfirstlane(((int)part * NW + wave) * KBW);
   int nkb = kb_tot - kb0;  // valid k-blocks of this wave (wave-uniform)
   nkb = nkb < 0 ? 0 : (nkb > KBW ? KBW : nkb);
 
@@ -269,9 +288,7 @@ __global__ __launch_bounds__(NW * 64) void w4a16_decode_v2(W4Params p) {
       *(f32x4*)(mine + sl * 1024 + (4 * g + r) * 64 + 4 * c) =
           (f32x4){acc[sl][0][r], acc[sl][1][r], acc[sl][2][r], acc[sl][3][r]};
   __syncthreads();
-  for (int t = threadIdx.x; t < 256 * RS; t += NW * 64) {
-    const int C = t & 15, R = t >> 4;  // R: output row of this launch (slab R / 16)
-    const int so = (R >> 4) * 1024 + (R & 15) * 64 + 4 * C;
+  auto wave_sum = [&](int so) {
     f32x4 s4 = *(const f32x4*)(red + so);
 #pragma unroll
     for (int v = 1; v < NW; ++v) {
@@ -281,6 +298,73 @@ __global__ __launch_bounds__(NW * 64) void w4a16_decode_v2(W4Params p) {
       s4.z += t4.z;
       s4.w += t4.w;
     }
+    return s4;
+  };
+  if (XK && p.pieces > 1) {
+    // This piece's [16 x 64] partial -> its slot; the last piece of the strip
+    // sums the slots in piece order (its own from registers) and stores Y.
+    constexpr int SEG = (256 + NW * 64 - 1) / (NW * 64);  // row segments per thread
+    float* slots = p.xk.part + (size_t)strip * p.pieces * 1024;
+    f32x4 own[SEG];
+#pragma unroll
+    for (int i = 0; i < SEG; ++i) {
+      const int t = (int)threadIdx.x + i * NW * 64;
+      if (t < 256) {
+        own[i] = wave_sum((t >> 4) * 64 + 4 * (t & 15));
+        *(f32x4*)(slots + (size_t)part * 1024 + (t >> 4) * 64 + 4 * (t & 15)) = own[i];
+      }
+    }
+    if (!xk_arrive(p.xk, strip, p.pieces)) return;
+    // Every slot load is issued before the first add: loads under a branch
+    // would each wait at the branch join (the first XK build read 7 slots one
+    // after another, 10 us at config 4).  Slot indices past the piece count are
+    // clamped to the last slot and their values not added.
+    auto sum_slots = [&](auto pmax_c, int so, const f32x4& mine) {
+      constexpr int PMAX = decltype(pmax_c)::value;
+      f32x4 v[PMAX];
+#pragma unroll
+      for (int q = 0; q < PMAX; ++q) {
+        const int qq = q < (int)p.pieces ? q : (int)p.pieces - 1;
+        v[q] = *(const f32x4*)(slots + (size_t)qq * 1024 + so);
+      }
+      f32x4 s4 = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int q = 0; q < PMAX; ++q) {
+        const f32x4 t4 = q == (int)part ? mine : v[q];
+        if (q < (int)p.pieces) {
+          s4.x += t4.x;
+          s4.y += t4.y;
+          s4.z += t4.z;
+          s4.w += t4.w;
+        }
+      }
+      return s4;
+    };
+#pragma unroll
+    for (int i = 0; i < SEG; ++i) {
+      const int t = (int)threadIdx.x + i * NW * 64;
+      if (t >= 256) continue;
+      const int C = t & 15, R = t >> 4, so = R * 64 + 4 * C;
+      // pieces <= 16 (kXkMaxPieces on the host)
+      const f32x4 s4 = p.pieces <= 8 ? sum_slots(std::integral_constant<int, 8>{}, so, own[i])
+                                     : sum_slots(std::integral_constant<int, 16>{}, so, own[i]);
+      const int col = n0 + 4 * C;
+      if (R >= (int)p.M || col >= (int)p.N) continue;
+      if (p.out_bf16) {
+        *(u32x2*)((uint16_t*)p.y + (size_t)R * p.N + col) = u32x2{pack_bf16x2(s4.x, s4.y), pack_bf16x2(s4.z, s4.w)};
+      } else {
+        f32x2_t* o = (f32x2_t*)((float*)p.y + (size_t)R * p.N + col);
+        o[0] = f32x2_t{s4.x, s4.y};
+        o[1] = f32x2_t{s4.z, s4.w};
+      }
+    }
+    xk_reset(p.xk, strip);
+    return;
+  }
+  for (int t = threadIdx.x; t < 256 * RS; t += NW * 64) {
+    const int C = t & 15, R = t >> 4;  // R: output row of this launch (slab R / 16)
+    const int so = (R >> 4) * 1024 + (R & 15) * 64 + 4 * C;
+    const f32x4 s4 = wave_sum(so);
     const int col = n0 + 4 * C;
     if (R >= (int)p.M || col >= (int)p.N) continue;
     if (p.out_bf16 && gridDim.y == 1) {

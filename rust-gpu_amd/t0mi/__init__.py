@@ -184,6 +184,7 @@ SIGNATURES = {
     "t0mi_recycle": (_I, [_P, _U64]),
     "t0mi_pool_cached_bytes": (_SZ, [_P]),
     "t0mi_pool_clear": (_I, [_P]),
+    "t0mi_xcd_placement": (_I, [_P, ctypes.POINTER(_U32), ctypes.POINTER(_U32)]),
     "t0mi_h2d": (_I, [_P, _U64, _P, _SZ]),
     "t0mi_d2h": (_I, [_P, _P, _U64, _SZ]),
     "t0mi_memset": (_I, [_P, _U64, _I, _SZ]),
@@ -642,6 +643,13 @@ class Runtime:
 
     def pool_clear(self):
         check(lib().t0mi_pool_clear(self.handle))
+
+    def xcd_placement(self):
+        """(XCDs the in-launch split-K exchange uses or 0, whether any exchange launch found a
+        workgroup on another XCD than planned)."""
+        n, bad = ctypes.c_uint32(), ctypes.c_uint32()
+        check(lib().t0mi_xcd_placement(self.handle, ctypes.byref(n), ctypes.byref(bad)))
+        return n.value, bool(bad.value)
 
     def h2d(self, dptr: int, host_bytes) -> None:
         import numpy as np

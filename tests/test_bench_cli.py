@@ -36,7 +36,8 @@ def test_traffic_figures_for_every_leg():
 
 @pytest.mark.gpu
 @pytest.mark.parametrize("leg,unit,bound", [("gemm", "TFLOPS", "mfma"), ("w4a16", "GB/s", "hbm"),
-                                            ("skinny", "GB/s", "hbm"), ("prefill", "TFLOPS", "mfma")])
+                                            ("skinny", "GB/s", "hbm"), ("prefill", "TFLOPS", "mfma"),
+                                            ("shard", "GB/s", "hbm")])
 def test_leg_prints_one_json_line(leg, unit, bound):
     r = run_bench("--only", leg, "--steps", "3", "--warmup", "1", "--no-cpu")
     assert r.returncode == 0, r.stderr[-2000:]
