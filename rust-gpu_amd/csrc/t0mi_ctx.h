@@ -142,6 +142,11 @@ bool auto_plan(uint32_t m, uint32_t n, uint32_t k, uint32_t transpose, uint32_t 
 int run_gemm_planned(t0mi_ctx* ctx, const AutoPlan& pl, uint32_t transpose, uint64_t x, uint64_t b, uint64_t y,
                      uint32_t m, uint32_t n, uint32_t k, uint32_t out_dtype = T0MI_OUT_F32, uint64_t bias = 0,
                      const EpiChain* epi = nullptr);
+// Split-K with the partials combined inside the launch (gemm_xk.hip): launches
+// when cfg's tile has an exchange kernel, the exchange is on and the grid fits
+// the GPU in one round (*launched = true); otherwise leaves the call to the
+// plane route.  p is the split-K GemmParams with Y the caller's output.
+int launch_gemm_xk(t0mi_ctx* ctx, const t0mi_gemm_config& cfg, GemmParams p, bool* launched);
 // Launches the bf16 GEMM kernel for (cfg, params) on ctx's stream.
 int launch_gemm(t0mi_ctx* ctx, const t0mi_gemm_config& cfg, const GemmLaunchEntry* e, GemmParams p);
 int check_ctx(t0mi_ctx* ctx);

@@ -943,6 +943,16 @@ int run_gemm(t0mi_ctx* ctx, const t0mi_gemm_config& cfg, const GemmLaunchEntry* 
     return set_error(T0MI_ERR_INVALID,
                      "%ux%u with split_k=%u needs %zu bytes of scratch; the fixed workspace holds %zu", m, n,
                      k == 0 ? 1u : sk, ws_need, fixed->cap);
+  if (k > 0 && sk > 1 && !fixed) {
+    // The exchange route first: it needs no plane workspace.
+    const uint32_t kt = (k + cfg.tile_k - 1) / cfg.tile_k;
+    GemmParams px = p;
+    px.k_per_split = ((kt + sk - 1) / sk) * cfg.tile_k;
+    px.y = (void*)y;
+    bool launched = false;
+    int rc = launch_gemm_xk(ctx, cfg, px, &launched);
+    if (rc || launched) return rc;
+  }
   void* ws = nullptr;
   if (ws_need) {
     if (fixed) {
@@ -967,7 +977,10 @@ int run_gemm(t0mi_ctx* ctx, const t0mi_gemm_config& cfg, const GemmLaunchEntry* 
     return launch_gemm(ctx, cfg, e, p);
   }
   // Split-K: partitions of whole K tiles write f32 planes into the workspace,
-  // then a reduce pass sums them in partition order.
+  // then a reduce pass sums them in partition order -- or, where the tile has
+  // an exchange kernel and the grid fits the GPU at once, the partitions meet
+  // in their XCD's L2 inside the one launch (bit-identical; not for a fixed
+  // workspace, whose callers allocate nothing).
   const uint32_t kt = (k + cfg.tile_k - 1) / cfg.tile_k;
   p.k_per_split = ((kt + sk - 1) / sk) * cfg.tile_k;
   p.y = ws;
