@@ -89,6 +89,17 @@ int run_gemm_persistent(t0mi_ctx* ctx, const t0mi_gemm_config& cfg, const GemmLa
   if (bias & 3) return set_error(T0MI_ERR_INVALID, "bias must be 4-byte aligned");
   const int nn = cfg.transpose == T0MI_NN;
   const char* route = persistent_route(cfg, m, n, k);
+  if (route[0] == 'd' && k > 0 && (nn || m > 16 || (uint64_t)n > 16ull * (uint64_t)ctx->cu_count)) {
+    // Decode-sized calls where the one-shot schedule auto_select picks for the
+    // same call is faster (MI355X, K = 4096, f32 out, direct launches: NN 1 / 16
+    // rows x 4096 13.2 / 13.6 us against 15.9 / 18.7; NT 32 / 64 rows x 4096
+    // 13.9 / 15.3 against 16.4 / 27.7; NT 16 x 11008, more 16-column units than
+    // CUs, 23.2 against 30.2 in a graph replay): that schedule runs, under the
+    // spec's name, kernargs and grid.  NT up to 16 rows and one round of units
+    // keeps the one-launch decode kernel (1 / 16 x 4096: 8.9 / 11.8 against
+    // 13.7 / 13.2 us).
+    return run_gemm_auto(ctx, cfg.transpose, x, b, y, m, n, k, cfg.out_dtype, bias, &epi);
+  }
   if (route[0] == 'o') {
     // A persistent spec of the caller's own whose tile has no persistent instantiation:
     // the same tile's one-shot kernel, one plane (split-K is not part of a persistent run).

@@ -12,6 +12,7 @@
 // poisons the runtime — and turns it into a hipLaunchKernelGGL on the
 // runtime's stream.
 #include <sched.h>
+#include <tuple>
 #include <string.h>
 #include <time.h>
 
@@ -1051,10 +1052,42 @@ bool t0mi::auto_plan(uint32_t m, uint32_t n, uint32_t k, uint32_t transpose, uin
   return false;
 }
 
+namespace {
+// auto_plan results by shape (the ranking walks every prebuilt variant and
+// split: microseconds of host time per call otherwise).  Process-wide, like
+// cached_auto_select's cache; cleared when it grows past kPlanCacheMax.
+struct PlanKey {
+  uint32_t m, n, k, transpose, out_dtype, cus;
+  bool operator<(const PlanKey& o) const {
+    return std::tie(m, n, k, transpose, out_dtype, cus) < std::tie(o.m, o.n, o.k, o.transpose, o.out_dtype, o.cus);
+  }
+};
+constexpr size_t kPlanCacheMax = 4096;
+std::mutex g_plan_mu;
+std::map<PlanKey, AutoPlan> g_plans;
+bool cached_auto_plan(uint32_t m, uint32_t n, uint32_t k, uint32_t transpose, uint32_t out_dtype, uint32_t cus,
+                      AutoPlan* pl) {
+  const PlanKey key{m, n, k, transpose, out_dtype, cus};
+  {
+    std::lock_guard<std::mutex> lk(g_plan_mu);
+    auto it = g_plans.find(key);
+    if (it != g_plans.end()) {
+      *pl = it->second;
+      return true;
+    }
+  }
+  if (!t0mi::auto_plan(m, n, k, transpose, out_dtype, cus, pl)) return false;
+  std::lock_guard<std::mutex> lk(g_plan_mu);
+  if (g_plans.size() >= kPlanCacheMax) g_plans.clear();
+  g_plans[key] = *pl;
+  return true;
+}
+}  // namespace
+
 int t0mi::run_gemm_auto(t0mi_ctx* ctx, uint32_t transpose, uint64_t x, uint64_t b, uint64_t y, uint32_t m, uint32_t n,
                         uint32_t k, uint32_t out_dtype, uint64_t bias, const EpiChain* epi) {
   AutoPlan pl;
-  if (!auto_plan(m, n, k, transpose, out_dtype, (uint32_t)ctx->cu_count, &pl))
+  if (!cached_auto_plan(m, n, k, transpose, out_dtype, (uint32_t)ctx->cu_count, &pl))
     return set_error(T0MI_ERR_NO_KERNEL, "[t0mi] no prebuilt gfx950 kernel for %ux%ux%u (%s)", m, n, k,
                      transpose == T0MI_NN ? "NN" : "NT");
   return run_gemm_planned(ctx, pl, transpose, x, b, y, m, n, k, out_dtype, bias, epi);
