@@ -261,20 +261,25 @@ int t0mi_gemm(t0mi_ctx* ctx, const t0mi_gemm_config* cfg, uint64_t x, uint64_t b
  * growable workspace.  It calls no hipMalloc or hipFree.  A call needing more
  * than that (M * N * 4 * split_k bytes; M * N * 4 when K = 0) fails with
  * T0MI_ERR_INVALID before anything is launched.  Every runtime on one GPU
- * shares that GPU's array: calls that overlap on one GPU (two streams or two
- * runtimes) race; calls on one stream are ordered.  Nothing in the array needs
- * to start at zero.  Asynchronous. */
+ * shares that GPU's array: calls on one stream are ordered; a call from
+ * another stream while the last call's work on the GPU has not finished is
+ * refused with T0MI_ERR_INVALID (an event recorded after each call, made when
+ * the first runtime on the device was created); calls recorded into a graph
+ * are not tracked, and replays that overlap with other users of the array on
+ * one GPU race.  Nothing in the array needs to start at zero.  Asynchronous. */
 int t0mi_gemm_noalloc(t0mi_ctx* ctx, const t0mi_gemm_config* cfg, uint64_t x, uint64_t b, uint64_t y,
                       uint64_t bias, uint32_t m, uint32_t n, uint32_t k);
 
 /* No counterpart in the reference (RDNA parts have one L2).  The XCD count of
- * this runtime's device when the in-launch split-K exchange is on (workgroup i
- * of a launch was found on XCD i % n for every i by a probe at runtime
- * creation), or 0 when it is off and the kernels that use it fall back to
- * split-K planes summed by a second launch; and, when `misplaced` is not null,
- * whether any exchange launch on this runtime found one of its workgroups on
- * another XCD than planned (its result would then be wrong; waits for the
- * stream).  For tests and callers that check what runs. */
+ * this runtime's device when the W4A16 decode's in-launch split-K exchange is
+ * on (workgroup i of a launch was found on XCD i % n for every i by a probe at
+ * runtime creation), or 0 when it is off and the decode keeps one workgroup per
+ * column strip; and, when `misplaced` is not null, whether an exchange launch
+ * on this runtime has found one of its workgroups on another XCD than the
+ * numbering planned (waits for the stream).  Informational: the partials are
+ * written through to memory, so results do not depend on where the pieces
+ * ran; a misplaced piece only costs its reader an L2 miss.  For tests and
+ * callers that check what runs. */
 int t0mi_xcd_placement(t0mi_ctx* ctx, uint32_t* n_xcd, uint32_t* misplaced);
 
 /* ---- batched submission: DispatchQueue (src/t0/prefill_dispatch.rs:58-214) - */

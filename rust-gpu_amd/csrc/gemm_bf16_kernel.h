@@ -38,7 +38,6 @@
 
 #include "epi_chain.h"
 #include "index_maps.h"
-#include "xcd_exchange.h"
 
 namespace t0mi {
 
@@ -83,11 +82,6 @@ struct GemmParams {
   uint32_t xcd_remap;     // 1: make tiles that share an XCD (L2) contiguous
   uint32_t stream_out;    // 1: staged bf16 stores are non-temporal (set when all
                           // workgroups run at once, so every store comes at the end)
-  // gemm_bf16_xk_kernel only: the split-K partials meet in one XCD's L2 (see
-  // xk_gemm_epilogue); the longest a piece waits for the others, in
-  // s_memrealtime ticks (100 MHz).
-  XcdExchange xk;
-  uint64_t xk_wait_ticks;
 };
 
 __device__ __forceinline__ uint16_t f32_to_bf16_rne(float f) {
@@ -372,16 +366,10 @@ struct GemmTile {
   static_assert(!EVEN || LPT * (S - 1) <= 63, "vmcnt range");
 };
 
-template <int BM, int BN, int WM, int WN, int FM, int FN>
-__device__ __forceinline__ void xk_gemm_epilogue(const GemmParams& p, const f32x16 (&acc)[FN][FM], uint32_t tile,
-                                                 int piece, int m0, int n0, int wm, int wn, int lane);
-
 // One output tile (tm, tn) of K partition `part`: the whole kernel body, called
-// once by gemm_bf16_kernel and in a loop by the persistent kernel.  XK: the
-// partition's partial goes through the in-launch exchange of tile `xtile`
-// (gemm_bf16_xk_kernel) instead of a plane.
-template <int BM, int BN, int BK, int WM, int WN, int S, bool NN, bool XK = false>
-__device__ __forceinline__ void gemm_bf16_tile(const GemmParams& p, int tm, int tn, int part, uint32_t xtile = 0) {
+// once by gemm_bf16_kernel and in a loop by the persistent kernel.
+template <int BM, int BN, int BK, int WM, int WN, int S, bool NN>
+__device__ __forceinline__ void gemm_bf16_tile(const GemmParams& p, int tm, int tn, int part) {
   using T = GemmTile<BM, BN, BK, WM, WN, S, NN>;
   constexpr int FM = T::FM, FN = T::FN, KC = T::KC, KS = T::KS, NC = T::NC;
   constexpr int TM = T::TM, TN = T::TN;
@@ -718,10 +706,6 @@ __device__ __forceinline__ void gemm_bf16_tile(const GemmParams& p, int tm, int 
   // i.e. four consecutive columns per (lane, g): one 16-byte (f32) or
   // 8-byte (bf16) store.  The (fm, fn) loops are expanded at compile time so
   // acc is only ever indexed by constants and stays in registers.
-  if constexpr (XK) {
-    xk_gemm_epilogue<BM, BN, WM, WN, FM, FN>(p, acc, xtile, part, m0, n0, wm, wn, lane);
-    return;
-  }
   const bool partial_plane = p.split_k > 1;
   char* ybase = (char*)p.y + (partial_plane ? (size_t)part * p.y_split_stride : 0);
   // Full tiles with bf16 output: stage each wave's block through the (now
@@ -751,130 +735,6 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_bf16_kernel(GemmParams p) {
   int tm, tn, part;
   tile_coords(p, tm, tn, part);
   gemm_bf16_tile<BM, BN, BK, WM, WN, S, NN>(p, tm, tn, part);
-}
-
-// Split-K with the partials combined inside the launch (xcd_exchange.h): the
-// split_k pieces of an output tile are numbered onto the tile's XCD; after its
-// K loop each piece stores its fp32 partial into its slot in that XCD's L2,
-// arrives on the tile's counter and waits (bounded by p.xk_wait_ticks) until
-// all pieces have arrived; piece q then sums its 1/split_k share of the
-// tile's valid rows over the split_k slots in piece order, applies the
-// epilogue and stores Y; the last piece to leave resets the counters.  Every
-// piece of a tile must be resident at once: the host launches it only when the
-// whole grid fits the GPU in one round.  Results are bit-identical to the
-// plane route (same per-piece sums, same order of the final adds, same
-// epilogue and rounding).
-template <int BM, int BN, int BK, int WM, int WN, int S, bool NN>
-__global__ __launch_bounds__(WM * WN * 64) void gemm_bf16_xk_kernel(GemmParams p) {
-  uint32_t tile, piece;
-  xk_unpack(blockIdx.x, p.xk.nx, p.split_k, &tile, &piece);
-  if (tile >= p.tiles_m * p.tiles_n) return;  // the numbering's padding (whole workgroup)
-  xk_check_placement(p.xk);
-  gemm_bf16_tile<BM, BN, BK, WM, WN, S, NN, true>(p, (int)(tile / p.tiles_n), (int)(tile % p.tiles_n), (int)piece,
-                                                  tile);
-}
-
-template <int BM, int BN, int WM, int WN, int FM, int FN>
-__device__ __forceinline__ void xk_gemm_epilogue(const GemmParams& p, const f32x16 (&acc)[FN][FM], uint32_t tile,
-                                                 int piece, int m0, int n0, int wm, int wn, int lane) {
-  constexpr int TM = BM / WM, TN = BN / WN, NTHR = WM * WN * 64, TILE = BM * BN;
-  const int P = (int)p.split_k;
-  float* slots = p.xk.part + (size_t)tile * P * TILE;
-  // 1. This piece's partial -> its slot, row-major [BM][BN]: lane l of block
-  //    (fn, fm) holds rows fm*32 + (l & 31), columns fn*32 + 8g + 4*(l >> 5) + 0..3.
-  {
-    float* mine = slots + (size_t)piece * TILE;
-    const int lrow = lane & 31, lhalf = lane >> 5;
-    static_for<FM>([&](auto fmc) {
-      constexpr int fm = decltype(fmc)::value;
-      static_for<FN>([&](auto fnc) {
-        constexpr int fn = decltype(fnc)::value;
-        const int r = wm * TM + fm * 32 + lrow;
-        if (m0 + r < (int)p.M) {  // rows past M are never summed: not stored
-#pragma unroll
-          for (int g = 0; g < 4; ++g) {
-            const int c = wn * TN + fn * 32 + 8 * g + 4 * lhalf;
-            *(f32x4*)(mine + r * BN + c) =
-                f32x4{acc[fn][fm][4 * g], acc[fn][fm][4 * g + 1], acc[fn][fm][4 * g + 2], acc[fn][fm][4 * g + 3]};
-          }
-        }
-      });
-    });
-  }
-  // 2. Arrive; wait until every piece of the tile has (thread 0 polls the
-  //    counter with atomics, which execute where the other pieces' do).
-  uint32_t* arrive = xk_counter(p.xk, tile);
-  uint32_t* depart = arrive + 1;
-  __shared__ uint32_t all_in;
-  asm volatile("" ::: "memory");
-  __builtin_amdgcn_s_waitcnt(0);  // this thread's partial stores are in L2
-  __syncthreads();
-  if (threadIdx.x == 0) {
-    uint32_t n = __hip_atomic_fetch_add(arrive, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) + 1;
-    const uint64_t t0 = __builtin_amdgcn_s_memrealtime();
-    while (n < (uint32_t)P) {
-      if (__builtin_amdgcn_s_memrealtime() - t0 > p.xk_wait_ticks) break;
-      __builtin_amdgcn_s_sleep(2);
-      n = __hip_atomic_fetch_add(arrive, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    }
-    all_in = n >= (uint32_t)P;
-    if (!all_in) atomicOr(p.xk.flag, 2u);  // a piece never arrived: Y rows of this slice are not written
-  }
-  __syncthreads();
-  // 3. The tile's valid rows (min(BM, M - m0)) as runs of 8 columns, split
-  //    evenly over the pieces: piece q sums its runs over the P slots in piece
-  //    order (every slot load issued before the first add), applies the
-  //    epilogue and stores them.
-  if (all_in) {
-    const int rows = (int)p.M - m0 < BM ? (int)p.M - m0 : BM;
-    const int runs = rows * (BN / 8), r0 = piece * runs / P, r1 = (piece + 1) * runs / P;
-    auto sum_slots = [&](auto pmax_c, int off) {
-      constexpr int PMAX = decltype(pmax_c)::value;
-      f32x4 lo[PMAX], hi[PMAX];
-#pragma unroll
-      for (int q = 0; q < PMAX; ++q) {
-        const int qq = q < P ? q : P - 1;
-        lo[q] = *(const f32x4*)(slots + (size_t)qq * TILE + off);
-        hi[q] = *(const f32x4*)(slots + (size_t)qq * TILE + off + 4);
-      }
-      f32x4 a = lo[0], b = hi[0];
-#pragma unroll
-      for (int q = 1; q < PMAX; ++q)
-        if (q < P) {
-          a += lo[q];
-          b += hi[q];
-        }
-      return std::make_pair(a, b);
-    };
-    for (int v = r0 + (int)threadIdx.x; v < r1; v += NTHR) {
-      const int r = v / (BN / 8), c = (v % (BN / 8)) * 8;
-      const int m = m0 + r, n = n0 + c;
-      if (n >= (int)p.N) continue;  // N % 8 == 0: the 8 columns are all in range or all out
-      const auto ab = P <= 8 ? sum_slots(std::integral_constant<int, 8>{}, r * BN + c)
-                             : sum_slots(std::integral_constant<int, 16>{}, r * BN + c);
-      float o[8] = {ab.first.x, ab.first.y, ab.first.z, ab.first.w, ab.second.x, ab.second.y, ab.second.z,
-                    ab.second.w};
-      if (p.epi.n) {
-#pragma unroll
-        for (int j = 0; j < 8; ++j) o[j] = epi_apply(o[j], p.bias ? p.bias[n + j] : 0.0f, p.epi);
-      }
-      if (p.out_bf16) {
-        *(u32x4*)((uint16_t*)p.y + (size_t)m * p.ldy + n) =
-            u32x4{pack_bf16x2(o[0], o[1]), pack_bf16x2(o[2], o[3]), pack_bf16x2(o[4], o[5]), pack_bf16x2(o[6], o[7])};
-      } else {
-        f32x4* yp = (f32x4*)((float*)p.y + (size_t)m * p.ldy + n);
-        yp[0] = f32x4{o[0], o[1], o[2], o[3]};
-        yp[1] = f32x4{o[4], o[5], o[6], o[7]};
-      }
-    }
-  }
-  // 4. Depart: the last piece to leave (every piece is past its wait) resets
-  //    both counters for the next launch.
-  if (threadIdx.x == 0 &&
-      __hip_atomic_fetch_add(depart, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == (uint32_t)P - 1) {
-    __hip_atomic_store(arrive, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    __hip_atomic_store(depart, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  }
 }
 
 }  // namespace t0mi

@@ -92,9 +92,9 @@ struct t0mi_ctx {
   uint32_t last_grid[3] = {0, 0, 0};
   std::vector<uint8_t> last_ka;
   int cu_count = 256;
-  // In-launch split-K exchange through one XCD's L2 (xcd_exchange.h): the XCD
+  // In-launch split-K exchange of the W4A16 decode (xcd_exchange.h): the XCD
   // count when the placement probe found workgroup i on XCD i % xk_nx for every
-  // i (0: the probe failed; kernels then keep their split-K planes), the
+  // i (0: the probe failed; the decode then keeps one workgroup per strip), the
   // counters (xk_nx groups of kXkCountersPerXcd, zeroed once, left zeroed by
   // every launch), the misplacement flag after them, and the partial slots.
   uint32_t xk_nx = 0;
@@ -142,11 +142,6 @@ bool auto_plan(uint32_t m, uint32_t n, uint32_t k, uint32_t transpose, uint32_t 
 int run_gemm_planned(t0mi_ctx* ctx, const AutoPlan& pl, uint32_t transpose, uint64_t x, uint64_t b, uint64_t y,
                      uint32_t m, uint32_t n, uint32_t k, uint32_t out_dtype = T0MI_OUT_F32, uint64_t bias = 0,
                      const EpiChain* epi = nullptr);
-// Split-K with the partials combined inside the launch (gemm_xk.hip): launches
-// when cfg's tile has an exchange kernel, the exchange is on and the grid fits
-// the GPU in one round (*launched = true); otherwise leaves the call to the
-// plane route.  p is the split-K GemmParams with Y the caller's output.
-int launch_gemm_xk(t0mi_ctx* ctx, const t0mi_gemm_config& cfg, GemmParams p, bool* launched);
 // Launches the bf16 GEMM kernel for (cfg, params) on ctx's stream.
 int launch_gemm(t0mi_ctx* ctx, const t0mi_gemm_config& cfg, const GemmLaunchEntry* e, GemmParams p);
 int check_ctx(t0mi_ctx* ctx);

@@ -339,6 +339,32 @@ static int scratch_for_device(int dev, void** out) {
   return T0MI_OK;
 }
 
+// Who used this device's scratch last: the stream of the last
+// t0mi_gemm_noalloc call on the device and an event recorded after its
+// launches.  A call from another stream while that event has not completed
+// would overwrite planes still being summed: it is refused instead.  The
+// event is made at set-up (the first runtime created on the device), so the
+// entry point itself creates nothing.
+struct ScratchUse {
+  std::mutex mu;
+  hipStream_t last = nullptr;
+  hipEvent_t done = nullptr;
+  bool recorded = false;
+};
+static ScratchUse* scratch_use_for_device(int dev, bool create) {
+  static std::mutex mu;
+  static std::map<int, ScratchUse*> known;  // held until the process ends, like the scratch itself
+  std::lock_guard<std::mutex> lock(mu);
+  auto it = known.find(dev);
+  if (it != known.end()) return it->second;
+  if (!create) return nullptr;
+  ScratchUse* u = new ScratchUse();
+  if (hipEventCreateWithFlags(&u->done, hipEventDisableTiming) != hipSuccess) u->done = nullptr;
+  (void)hipGetLastError();
+  known.emplace(dev, u);
+  return u;
+}
+
 // ------------------------------------------------ XCD placement probe ----
 
 // Workgroup i records the XCD it runs on.
@@ -439,6 +465,7 @@ static int ctx_create(int device, bool use_given_stream, void* hip_stream, t0mi_
   }
   // A failed lookup leaves the runtime usable; only t0mi_gemm_noalloc reports it.
   c->scratch_rc = scratch_for_device(dev, &c->scratch);
+  (void)scratch_use_for_device(dev, true);
   c->xk_nx = placement_for_device(dev);
   *out = c;
   return T0MI_OK;
@@ -944,16 +971,6 @@ int run_gemm(t0mi_ctx* ctx, const t0mi_gemm_config& cfg, const GemmLaunchEntry* 
     return set_error(T0MI_ERR_INVALID,
                      "%ux%u with split_k=%u needs %zu bytes of scratch; the fixed workspace holds %zu", m, n,
                      k == 0 ? 1u : sk, ws_need, fixed->cap);
-  if (k > 0 && sk > 1 && !fixed) {
-    // The exchange route first: it needs no plane workspace.
-    const uint32_t kt = (k + cfg.tile_k - 1) / cfg.tile_k;
-    GemmParams px = p;
-    px.k_per_split = ((kt + sk - 1) / sk) * cfg.tile_k;
-    px.y = (void*)y;
-    bool launched = false;
-    int rc = launch_gemm_xk(ctx, cfg, px, &launched);
-    if (rc || launched) return rc;
-  }
   void* ws = nullptr;
   if (ws_need) {
     if (fixed) {
@@ -978,10 +995,7 @@ int run_gemm(t0mi_ctx* ctx, const t0mi_gemm_config& cfg, const GemmLaunchEntry* 
     return launch_gemm(ctx, cfg, e, p);
   }
   // Split-K: partitions of whole K tiles write f32 planes into the workspace,
-  // then a reduce pass sums them in partition order -- or, where the tile has
-  // an exchange kernel and the grid fits the GPU at once, the partitions meet
-  // in their XCD's L2 inside the one launch (bit-identical; not for a fixed
-  // workspace, whose callers allocate nothing).
+  // then a reduce pass sums them in partition order.
   const uint32_t kt = (k + cfg.tile_k - 1) / cfg.tile_k;
   p.k_per_split = ((kt + sk - 1) / sk) * cfg.tile_k;
   p.y = ws;
@@ -1026,7 +1040,26 @@ extern "C" int t0mi_gemm_noalloc(t0mi_ctx* ctx, const t0mi_gemm_config* cfg, uin
   const GemmLaunchEntry* e = find_gemm_launch(phys);
   if (!e) return set_error(T0MI_ERR_NO_KERNEL, "[t0mi] no prebuilt gfx950 kernel for '%s'", config_name(*cfg).c_str());
   const FixedWorkspace fixed{ctx->scratch, (size_t)T0MI_NOALLOC_SCRATCH_BYTES};
-  return run_gemm(ctx, phys, e, x, b, y, bias, m, n, k, chain_of(cfg->epilogue), &fixed);
+  ScratchUse* u = ctx->null_backend ? nullptr : scratch_use_for_device(ctx->device, false);
+  if (!u || !u->done) return run_gemm(ctx, phys, e, x, b, y, bias, m, n, k, chain_of(cfg->epilogue), &fixed);
+  std::lock_guard<std::mutex> lk(u->mu);
+  hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+  (void)hipStreamIsCapturing(ctx->stream, &cap);
+  const bool capturing = cap != hipStreamCaptureStatusNone;  // captured calls are not tracked
+  if (!capturing && u->recorded && u->last != ctx->stream) {
+    const hipError_t q = hipEventQuery(u->done);
+    if (q == hipErrorNotReady)
+      return set_error(T0MI_ERR_INVALID,
+                       "t0mi_gemm_noalloc: device %d's scratch is still in use by a call on another stream; calls "
+                       "that overlap on one GPU would race (wait for that stream first)",
+                       ctx->device);
+  }
+  rc = run_gemm(ctx, phys, e, x, b, y, bias, m, n, k, chain_of(cfg->epilogue), &fixed);
+  if (rc == T0MI_OK && !capturing && hipEventRecord(u->done, ctx->stream) == hipSuccess) {
+    u->last = ctx->stream;
+    u->recorded = true;
+  }
+  return rc;
 }
 
 bool t0mi::auto_plan(uint32_t m, uint32_t n, uint32_t k, uint32_t transpose, uint32_t out_dtype, uint32_t cus,

@@ -304,14 +304,14 @@ __global__ __launch_bounds__(NW * 64) void w4a16_decode_v2(W4Params p) {
     // This piece's [16 x 64] partial -> its slot; the last piece of the strip
     // sums the slots in piece order (its own from registers) and stores Y.
     constexpr int SEG = (256 + NW * 64 - 1) / (NW * 64);  // row segments per thread
-    float* slots = p.xk.part + (size_t)strip * p.pieces * 1024;
+    const auto slots = xk_slots(p.xk.part + (size_t)strip * p.pieces * 1024, p.pieces * 4096u);
     f32x4 own[SEG];
 #pragma unroll
     for (int i = 0; i < SEG; ++i) {
       const int t = (int)threadIdx.x + i * NW * 64;
       if (t < 256) {
         own[i] = wave_sum((t >> 4) * 64 + 4 * (t & 15));
-        *(f32x4*)(slots + (size_t)part * 1024 + (t >> 4) * 64 + 4 * (t & 15)) = own[i];
+        xk_store(slots, (part * 1024u + (t >> 4) * 64u + 4u * (t & 15)) * 4u, own[i]);
       }
     }
     if (!xk_arrive(p.xk, strip, p.pieces)) return;
@@ -325,7 +325,7 @@ __global__ __launch_bounds__(NW * 64) void w4a16_decode_v2(W4Params p) {
 #pragma unroll
       for (int q = 0; q < PMAX; ++q) {
         const int qq = q < (int)p.pieces ? q : (int)p.pieces - 1;
-        v[q] = *(const f32x4*)(slots + (size_t)qq * 1024 + so);
+        v[q] = xk_load(slots, (uint32_t)(qq * 1024 + so) * 4u);
       }
       f32x4 s4 = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll

@@ -645,8 +645,9 @@ class Runtime:
         check(lib().t0mi_pool_clear(self.handle))
 
     def xcd_placement(self):
-        """(XCDs the in-launch split-K exchange uses or 0, whether any exchange launch found a
-        workgroup on another XCD than planned)."""
+        """(XCDs the W4A16 decode's in-launch split-K exchange uses or 0, whether an exchange
+        launch found a workgroup on another XCD than its numbering planned).  The second is
+        informational: the partials are written through to memory, results do not depend on it."""
         n, bad = ctypes.c_uint32(), ctypes.c_uint32()
         check(lib().t0mi_xcd_placement(self.handle, ctypes.byref(n), ctypes.byref(bad)))
         return n.value, bool(bad.value)

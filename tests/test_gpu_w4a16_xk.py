@@ -1,11 +1,12 @@
 """GPU tests of the W4A16 decode with its K range split over workgroups inside one launch
-(w4a16_decode_v2 with XK: the pieces of a 64-column strip meet in the strip's XCD's L2 and
-the last piece sums them in piece order).
+(w4a16_decode_v2 with XK: the pieces of a 64-column strip are numbered onto the strip's XCD,
+store their partials and the last piece sums them in piece order).
 
 Bars: against the exact-dequant oracle within max|err| <= 1e-2 * sqrt(K) * max|a| * max|w|
 and relative Frobenius error <= 1e-5 (f32 out); bit-identical results for repeated calls,
 across shapes that reuse the exchange counters, and across HIP-graph replays (the counters
-reset themselves); no workgroup found on another XCD than planned.
+reset themselves).  Where a workgroup runs is only reported: the slots are written through
+to memory, so the bars hold wherever the pieces ran.
 """
 import numpy as np
 import pytest
@@ -41,6 +42,14 @@ def dev_args(a, w, s, z):
     return bufs, (bufs[0][1], bufs[1][1], bufs[2][1], pz)
 
 
+def xk_state(r):
+    # The exchange is on.  A workgroup on another XCD than planned is only reported (its
+    # partials then cross XCDs through memory): the results checked are what matters.
+    n, misplaced = r.xcd_placement()
+    print(f"[xk] xcds={n} misplaced={misplaced}", flush=True)
+    return n == 8
+
+
 def check_oracle(y, a, w, s, z, k, group, zp=8, rel_max=1e-5):
     ref = oracle.w4a16_gemm(a, w, s, z, group, zp)
     tol = oracle.gemm_tolerance(k, oracle.bf16_to_f32(a), oracle.dequant_qweight_f32(w, s, z, group, zp))
@@ -49,9 +58,9 @@ def check_oracle(y, a, w, s, z, k, group, zp=8, rel_max=1e-5):
 
 
 def test_placement_probe_found_the_xcds(rt):
-    n, bad = rt.xcd_placement()
+    n, misplaced = rt.xcd_placement()
+    print(f"[xk] xcds={n} misplaced={misplaced}", flush=True)
     assert n == 8, "MI355X: 8 XCDs, workgroup i on XCD i % 8"
-    assert not bad
 
 
 @pytest.mark.parametrize("m,k,n,group,zeros", [
@@ -76,7 +85,7 @@ def test_decode_xk_vs_oracle(rt, m, k, n, group, zeros):
     rt.w4a16_gemm(pa, pw, ps, pz, 8, pb, m, k, n, group, t0mi.OUT_BF16)
     yb = oracle.bf16_to_f32(from_dev(db, np.uint16, (m, n)))
     check_oracle(yb, a, w, s, z, k, group, rel_max=5e-3)
-    assert rt.xcd_placement() == (8, False)
+    assert xk_state(rt)
 
 
 def test_counters_reset_across_shapes(rt):
@@ -131,6 +140,6 @@ def test_graph_replays_match_eager():
             assert r.wait_idle() == t0mi.OK
             assert np.array_equal(from_dev(side, np.uint16, (m, n)), ref), rep
         graph.destroy()
-        assert r.xcd_placement() == (8, False)
+        assert xk_state(r)
     finally:
         r.close()

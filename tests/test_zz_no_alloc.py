@@ -138,3 +138,36 @@ def test_too_large_is_refused_before_launch(rt):
     dy = call(rt, rt.gemm_noalloc, SPLITK_BF16, pa, pb, m, n, k)
     y_ref = result(call(rt, rt.gemm, SPLITK_BF16, pa, pb, m, n, k), SPLITK_BF16, m, n)
     assert np.array_equal(result(dy, SPLITK_BF16, m, n), y_ref)
+
+
+def test_overlapping_call_from_another_stream_is_refused():
+    """The scratch is shared by every runtime on the GPU: a call from a second stream while
+    the first stream's call is still queued or running is refused (T0MI_ERR_INVALID); once
+    that stream has drained, the second stream's call runs and matches t0mi_gemm."""
+    r1, r2 = t0mi.Runtime(device=0), t0mi.Runtime(device=0)  # two runtimes, each its own stream
+    try:
+        m, n, k = 128, 4096, 4096
+        a, b = operands(m, n, k, 40)
+        (da, pa), (db, pb) = to_dev(a), to_dev(b)
+        big_a, big_b = operands(4096, 4096, 4096, 41)
+        (dba, pba), (dbb, pbb) = to_dev(big_a), to_dev(big_b)
+        dbig, pbig = empty_dev(4096 * 4096 * 2)
+        big = t0mi.auto_select_layout(4096, 4096, 4096, t0mi.NN, t0mi.OUT_BF16)
+        torch().cuda.synchronize()
+        # ~1 ms of work queued on r1's stream ahead of its no-allocation call
+        for _ in range(10):
+            r1.gemm(big, pba, pbb, pbig, 4096, 4096, 4096)
+        d1 = call(r1, r1.gemm_noalloc, SPLITK_BF16, pa, pb, m, n, k)
+        with pytest.raises(t0mi.T0miError) as e:
+            call(r2, r2.gemm_noalloc, SPLITK_BF16, pa, pb, m, n, k)
+        assert e.value.code == t0mi.ERR_INVALID and "another stream" in str(e.value)
+        assert r1.wait_idle() == t0mi.OK
+        d2 = call(r2, r2.gemm_noalloc, SPLITK_BF16, pa, pb, m, n, k)
+        assert r2.wait_idle() == t0mi.OK
+        y1, y2 = result(d1, SPLITK_BF16, m, n), result(d2, SPLITK_BF16, m, n)
+        y_ref = result(call(r2, r2.gemm, SPLITK_BF16, pa, pb, m, n, k), SPLITK_BF16, m, n)
+        assert r2.wait_idle() == t0mi.OK
+        assert np.array_equal(y1, y_ref) and np.array_equal(y2, y_ref)
+    finally:
+        r1.close()
+        r2.close()
