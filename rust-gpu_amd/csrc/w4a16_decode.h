@@ -104,9 +104,10 @@ __device__ __forceinline__ float bf16f(uint32_t h) { return __builtin_bit_cast(f
 // XK (one slab): a 1-D grid of strips x p.pieces workgroups numbered for the
 // XCD exchange (xcd_exchange.h); piece c of a strip covers k-blocks
 // [c * NW * KBW, (c + 1) * NW * KBW).  With one piece the strip is stored
-// directly; otherwise the pieces' [16 x 64] fp32 partials meet in the strip's
-// XCD's L2 and the last piece sums them in piece order and stores Y, all in
-// this launch: every CU gets several workgroups however few strips N has.
+// directly; otherwise the pieces store their [16 x 64] fp32 partials with the
+// device-scope policy (normally all on the strip's XCD) and the last piece sums
+// them in piece order and stores Y, all in this launch: every CU gets several
+// workgroups however few strips N has.
 template <int NW, int KBW, int KBPG, bool ZEROS, int CH = 1, int RS = 1, bool XK = false>
 __global__ __launch_bounds__(NW * 64) void w4a16_decode_v2(W4Params p) {
   static_assert(KBW % KBPG == 0, "whole groups per wave");
