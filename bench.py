@@ -12,8 +12,15 @@ kernels are launched on (the t0mi runtime launches on torch's current stream).
 The W4A16 timing rotates over >= 512 MB of distinct weight copies so the
 256 MB Infinity Cache cannot serve repeats.
 
-Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--only gemm|w4a16|skinny|prefill] [--no-cpu]
-       [--config PRESET] [--tune]
+The default run also times, as extra keys of the same JSON line, config 3
+("skinny"), config 5 ("prefill": the default route, and "prefill_fused": the
+dequant inside the MFMA K loop) and the 16 x 4096 x 1376 W4A16 decode shard
+("shard"), each with its own roofline object and CPU baseline.
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--only LEG] [--no-cpu]
+       [--config PRESET] [--split-k S] [--stages S] [--tune] [--clocks] [--rows R]
+LEG: all (default) | gemm | w4a16 | skinny | prefill | shard (one leg alone) |
+     copy (FETCH/WRITE_SIZE calibration) | dispatch | persistent | split
 """
 import argparse
 import json

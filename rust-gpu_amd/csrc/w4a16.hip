@@ -430,12 +430,14 @@ static int launch_w4_pingpong(t0mi_ctx* ctx, uint64_t a, uint64_t qweight, uint6
 // One slab (m <= 16), groups 32..256, when N has too few 64-column strips to
 // give every CU one (strips * 2 <= CUs): the decode kernel with its K range
 // split over workgroups inside one launch (w4a16_decode_v2 with XK).  The
-// pieces of a strip are combined in the strip's XCD's L2 by the last piece to
-// arrive.  The largest power-of-two piece count up to 8 that keeps strips *
-// pieces <= CUs; a piece is nw waves of kbw k-blocks (whole groups).
+// pieces of a strip, numbered onto the strip's XCD, are combined by the last
+// piece to arrive through device-coherent partial slots (xcd_exchange.h).  The
+// largest power-of-two piece count up to 8 that keeps strips * pieces <= CUs;
+// a piece is nw waves of kbw k-blocks (whole groups).
 // Measured at K = 4096, group 128 (per call, against one workgroup per strip):
 // N = 1376 (the column-parallel shard of config 4 over 8 GPUs): 8 pieces of
-// 4 waves x 4 k-blocks, 4.90 against 7.36 us; N = 2752: 4 pieces of 8 x 4, 5.55
+// 4 waves x 4 k-blocks, 5.10 against 7.36 us (graph replay); with the slots
+// kept in L2 (not coherent across XCDs) N = 2752: 4 pieces of 8 x 4, 5.55
 // against 7.25 us; N = 5504: 2 pieces of 8 x 8, 6.88 against 7.36 us; N = 11008
 // (config 4): every split measured slower (9.3-10.8 us against 8.1: the
 // exchange's store, ticket and slot reads cost ~2 us under full HBM load), so
