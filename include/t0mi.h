@@ -473,7 +473,11 @@ int t0mi_auto_gemm(t0mi_ctx* ctx, uint64_t a, uint64_t b, uint64_t c, uint32_t m
  * Routes by row count: the decode kernel over 16-row slabs (exact dequant inside
  * the MFMA), several slabs per launch sharing one pass over the weights, in up to
  * three launches: up to 191 rows for group 128 (four slabs per launch), 144 for
- * groups 32 and 64, 96 for 256, 80 for other groups (one slab per launch); then
+ * groups 32 and 64, 96 for 256, 80 for other groups (one slab per launch; a
+ * single slab whose 64-column strips number at most half the CUs -- e.g. a
+ * column-parallel shard -- has each strip's K range split over up to 8
+ * workgroups, combined inside the launch through the runtime's exchange
+ * buffers); then
  * kernels that dequantize inside the MFMA K loop, rounding the weight once to
  * bf16: from there to 191 rows the 128x128 fused tile
  * kernel, 192..1535 rows (K and group multiples of 64) the 256x256 ping-pong

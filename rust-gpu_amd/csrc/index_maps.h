@@ -1,9 +1,10 @@
 // index_maps.h — the index maps of the gfx950 kernels: LDS swizzles, the
-// chunk each DMA lane fetches, and the activation slot map of the W4A16
-// decode kernel.  Plain constexpr integer functions, compiled into the kernels
+// chunk each DMA lane fetches, the activation slot map of the W4A16 decode
+// kernel, and the workgroup numbering of its in-launch K split.  Plain constexpr integer functions, compiled into the kernels
 // and, without HIP, into the host-side simulation that checks them (coverage
 // exactly once, LDS bijections, bank-conflict freedom; tests/index_maps_sim.cpp).
 #pragma once
+#include <stdint.h>
 
 #if defined(__HIPCC__)
 #define T0MI_HD __host__ __device__ __forceinline__
@@ -133,6 +134,19 @@ T0MI_HD constexpr int dec_slot(int h, int r, int x) {
 T0MI_HD constexpr int nn_pd_krow(int l) { return 8 * ((l >> 3) & 3) + 4 * (l >> 5) + ((l & 7) >> 1); }
 T0MI_HD constexpr int nn_pd_tr_off(int l, int h) {
   return h * 512 + (l >> 4) * 128 + ((l & 15) >> 2) * 32 + (l & 3) * 8;
+}
+
+// ---- in-launch split-K numbering (xcd_exchange.h) ------------------------------
+
+// Workgroup `id` of a launch whose tiles are each split over `pieces`
+// workgroups, numbered id = ((tile / nx) * pieces + piece) * nx + tile % nx so
+// that all pieces of a tile share id % nx (the XCD under round-robin dispatch):
+// (tile, piece) of `id`.  Tiles past the caller's count are the numbering's
+// padding to a multiple of nx.
+T0MI_HD void xk_unpack(uint32_t id, uint32_t nx, uint32_t pieces, uint32_t* tile, uint32_t* piece) {
+  const uint32_t xs = id % nx, r = id / nx;
+  *piece = r % pieces;
+  *tile = (r / pieces) * nx + xs;
 }
 
 }  // namespace t0mi

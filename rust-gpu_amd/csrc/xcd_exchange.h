@@ -31,6 +31,8 @@
 #pragma once
 #include <stdint.h>
 
+#include "index_maps.h"
+
 namespace t0mi {
 
 struct XcdExchange {
@@ -49,13 +51,7 @@ __device__ __forceinline__ uint32_t xcc_id() {
   return x;
 }
 
-// The workgroup numbering above, inverted: (tile, piece) of workgroup `id`.
-__device__ __forceinline__ void xk_unpack(uint32_t id, uint32_t nx, uint32_t pieces, uint32_t* tile,
-                                          uint32_t* piece) {
-  const uint32_t xs = id % nx, r = id / nx;
-  *piece = r % pieces;
-  *tile = (r / pieces) * nx + xs;
-}
+// xk_unpack, the workgroup numbering above inverted: index_maps.h.
 
 // Counter of `tile`.
 __device__ __forceinline__ uint32_t* xk_counter(const XcdExchange& x, uint32_t tile) {

@@ -422,6 +422,29 @@ static void persistent_nn_block() {
   }
 }
 
+// ---- in-launch split-K numbering (xk_unpack) -----------------------------------
+// Over the launch's grid (tiles rounded up to a multiple of nx, times pieces): every
+// (tile, piece) of the real tiles appears exactly once, padding ids name tiles past the
+// count, and every piece of a tile has the id modulo nx of the others (one XCD).
+static void xk_numbering(uint32_t tiles, uint32_t pieces, uint32_t nx) {
+  const uint32_t grid = (tiles + nx - 1) / nx * nx * pieces;
+  std::vector<int> seen((size_t)tiles * pieces, 0);
+  std::vector<int> xcd(tiles, -1);
+  for (uint32_t id = 0; id < grid; ++id) {
+    uint32_t t, pc;
+    xk_unpack(id, nx, pieces, &t, &pc);
+    CHECK(pc < pieces, "xk %u x%u nx %u: id %u -> piece %u", tiles, pieces, nx, id, pc);
+    if (t >= tiles) continue;  // padding
+    ++seen[(size_t)t * pieces + pc];
+    if (xcd[t] < 0) xcd[t] = (int)(id % nx);
+    CHECK(xcd[t] == (int)(id % nx), "xk %u x%u: tile %u on ids of residues %d and %u", tiles, pieces, t, xcd[t],
+          id % nx);
+  }
+  for (size_t i = 0; i < seen.size(); ++i)
+    CHECK(seen[i] == 1, "xk %u x%u nx %u: (tile %zu, piece %zu) taken %d times", tiles, pieces, nx, i / pieces,
+          i % pieces, seen[i]);
+}
+
 int main() {
   lds_rules();
   printf("%zu LDS rules fit the measurements\n", g_rules.size());
@@ -443,6 +466,9 @@ int main() {
   pingpong<false>();
   pingpong<true>();
   decode_slots();
+  for (uint32_t tiles : {1u, 7u, 22u, 90u, 171u, 256u})
+    for (uint32_t pieces : {1u, 2u, 3u, 8u, 16u})
+      for (uint32_t nx : {1u, 8u}) xk_numbering(tiles, pieces, nx);
   printf("%d checks, %d failures\n", g_checks, g_fail);
   return g_fail ? 1 : 0;
 }
