@@ -147,9 +147,12 @@ int t0mi_auto_schedule_gemm(uint32_t m, uint32_t n, uint32_t k, uint32_t transpo
  * *n_main < n, *tail over [*n_main, n) as a second launch.  The split is
  * planned when head's tiles fill some whole rounds of the GPU and part of one
  * more and the model expects the pair to be faster (e.g. 4096 x 14336 x 4096 NN:
- * 256x256 tiles over 12288 columns, the last 2048 on their own tile).  No
- * reference counterpart (cost_model.rs:464-534 ranks one configuration per
- * shape); for callers and tests that need to know what runs.  Host only. */
+ * 256x256 tiles over 12288 columns, the last 2048 on their own tile).  NT
+ * calls of 1..16 rows with K a multiple of 32 and N at most 16 x the CU count
+ * run the one-launch persistent decode kernel instead (faster there than any
+ * split-K schedule).  No reference counterpart (cost_model.rs:464-534 ranks one
+ * configuration per shape); for callers and tests that need to know what runs.
+ * Host only. */
 int t0mi_auto_gemm_plan(uint32_t m, uint32_t n, uint32_t k, uint32_t transpose, uint32_t out_dtype,
                         t0mi_gemm_config* head, uint32_t* n_main, t0mi_gemm_config* tail);
 /* auto_select_legacy (gemm_gen.rs:351-404), re-derived for gfx950. */

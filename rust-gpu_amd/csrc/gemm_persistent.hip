@@ -142,4 +142,36 @@ int run_gemm_persistent(t0mi_ctx* ctx, const t0mi_gemm_config& cfg, const GemmLa
   return T0MI_OK;
 }
 
+int run_gemm_decode_nt(t0mi_ctx* ctx, uint64_t x, uint64_t b, uint64_t y, uint32_t m, uint32_t n, uint32_t k,
+                       uint32_t out_dtype, uint64_t bias, const EpiChain& epi) {
+  if (m == 0 || m > 16 || k == 0 || k % 32 || n % 8 || (uint64_t)n > 16ull * (uint64_t)ctx->cu_count) return 1;
+  if ((uint64_t)m * k * 2 >= (1ull << 32) || (uint64_t)n * k * 2 >= (1ull << 32)) return 1;
+  // Argument errors are left to the caller's general route, which reports them.
+  if ((x | b | y) & 15 || bias & 3 || (chain_uses(epi, EOP_BIAS) && !bias)) return 1;
+  GemmParams p;
+  memset(&p, 0, sizeof p);
+  p.a = (const uint16_t*)x;
+  p.b = (const uint16_t*)b;
+  p.y = (void*)y;
+  p.bias = (const float*)bias;
+  p.M = m;
+  p.N = n;
+  p.K = k;
+  p.lda = k;
+  p.ldb = k;
+  p.ldy = n;
+  p.split_k = 1;
+  p.k_per_split = k;
+  p.out_bf16 = out_dtype == T0MI_OUT_BF16;
+  p.epi = epi;
+  p.xcd_remap = 1;
+  p.tiles_m = (m + PD_ROWS - 1) / PD_ROWS;
+  p.tiles_n = (n + PD_COLS - 1) / PD_COLS;
+  if (ctx->null_backend) return T0MI_OK;
+  launch_decode<false>(ctx, ctx->stream, p);
+  const hipError_t err = hipGetLastError();
+  if (err != hipSuccess) return set_error(T0MI_ERR_HIP, "decode GEMM launch: %s", hipGetErrorString(err));
+  return T0MI_OK;
+}
+
 }  // namespace t0mi

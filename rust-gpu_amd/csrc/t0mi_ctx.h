@@ -124,7 +124,8 @@ constexpr uint32_t kXkCounterStride = 64;  // u32s between counters
 int xk_prepare(t0mi_ctx* ctx, uint32_t tiles, size_t part_bytes, XcdExchange* x, bool* ok);
 // Runs a GEMM with the best prebuilt config for (m, n, k, transpose) and the
 // given output type (cost-model ranking, as t0mi_auto_select), as two launches
-// over column ranges where plan_column_split says so.  Asynchronous.
+// over column ranges where plan_column_split says so; NT calls of up to 16 rows
+// run the persistent decode kernel instead (run_gemm_decode_nt).  Asynchronous.
 int run_gemm_auto(t0mi_ctx* ctx, uint32_t transpose, uint64_t x, uint64_t b, uint64_t y, uint32_t m, uint32_t n,
                   uint32_t k, uint32_t out_dtype = T0MI_OUT_F32, uint64_t bias = 0, const EpiChain* epi = nullptr);
 // The schedule of an auto-scheduled GEMM: the ranking's first config with a
@@ -139,6 +140,13 @@ struct AutoPlan {
 bool auto_plan(uint32_t m, uint32_t n, uint32_t k, uint32_t transpose, uint32_t out_dtype, uint32_t cus,
                AutoPlan* pl);
 // Runs a plan made by auto_plan for the same (m, n, k, transpose, out_dtype).
+// Decode-sized NT GEMMs (1..16 rows, K a multiple of 32, N within one round of
+// 16-column units): the one-launch persistent decode kernel
+// (gemm_persistent.hip), which beats the split-K schedule there (1 / 16 x 4096
+// x 4096, f32 out: 8.5 / 11.5 against 13.6 / 12.4 us).  Returns 1, launching
+// nothing, when the call is outside that range or its arguments are invalid.
+int run_gemm_decode_nt(t0mi_ctx* ctx, uint64_t x, uint64_t b, uint64_t y, uint32_t m, uint32_t n, uint32_t k,
+                       uint32_t out_dtype, uint64_t bias, const EpiChain& epi);
 int run_gemm_planned(t0mi_ctx* ctx, const AutoPlan& pl, uint32_t transpose, uint64_t x, uint64_t b, uint64_t y,
                      uint32_t m, uint32_t n, uint32_t k, uint32_t out_dtype = T0MI_OUT_F32, uint64_t bias = 0,
                      const EpiChain* epi = nullptr);

@@ -1119,6 +1119,10 @@ bool cached_auto_plan(uint32_t m, uint32_t n, uint32_t k, uint32_t transpose, ui
 
 int t0mi::run_gemm_auto(t0mi_ctx* ctx, uint32_t transpose, uint64_t x, uint64_t b, uint64_t y, uint32_t m, uint32_t n,
                         uint32_t k, uint32_t out_dtype, uint64_t bias, const EpiChain* epi) {
+  if (transpose == T0MI_NT) {
+    const int rc = run_gemm_decode_nt(ctx, x, b, y, m, n, k, out_dtype, bias, epi ? *epi : EpiChain{});
+    if (rc <= 0) return rc;
+  }
   AutoPlan pl;
   if (!cached_auto_plan(m, n, k, transpose, out_dtype, (uint32_t)ctx->cu_count, &pl))
     return set_error(T0MI_ERR_NO_KERNEL, "[t0mi] no prebuilt gfx950 kernel for %ux%ux%u (%s)", m, n, k,

@@ -65,7 +65,9 @@ def test_matmul_forward(rt, m, k, n):
     check_gemm(y, oracle.gemm_bf16(xb, wb, "nn"), xb, wb, k)
 
 
-@pytest.mark.parametrize("m,k,n", [(16, 256, 128), (50, 512, 64)])
+# Up to 16 rows with K a multiple of 32 (the one-launch decode kernel): (16, 256, 128),
+# (1, 4096, 4096), (7, 2048, 11008), (16, 96, 136); 50 rows: the split-K schedule.
+@pytest.mark.parametrize("m,k,n", [(16, 256, 128), (50, 512, 64), (1, 4096, 4096), (7, 2048, 11008), (16, 96, 136)])
 def test_matmul_with_wt_bf16(rt, m, k, n):
     x = rand_f32((m, k), 3)
     wt = oracle.bf16_rne(rand_f32((n, k), 4))
