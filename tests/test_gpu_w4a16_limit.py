@@ -2,7 +2,8 @@
 more conversion buffer than the limit run the fused kernels (weights crossing HBM once, at 4 bits).
 
 Bars: the ping-pong fused kernel bit-identical to the dequant-once route at BASELINE config 5's
-full size (same bf16 rounding of each weight, same tile and k order); on a ragged shape, where the
+full size (same bf16 rounding of each weight, same tile and k order) and, there too, within the
+GEMM tolerance of the exact-dequant oracle over all outputs; on a ragged shape, where the
 dequant-once GEMM takes another tile and split, both routes within the GEMM tolerance; the 128x128
 fused tile kernel (groups that are not multiples of 64) within the GEMM tolerance of the oracle;
 a group no fused kernel takes refused with T0MI_ERR_INVALID when the limit forbids the buffer.
@@ -50,11 +51,21 @@ def run_both(rt, a, w, s, z, m, k, n, group, out_bf16):
 
 def test_config5_full_fused_bit_identical(rt):
     """BASELINE config 5 (4096 x 4096 x 14336, g128, per-group zeros, bf16 out): the fused
-    ping-pong kernel and the dequant-once route give the same bits."""
+    ping-pong kernel and the dequant-once route give the same bits, and the fused output is
+    also checked directly against the exact-dequant oracle, all 58.7M outputs (the whole
+    GEMM on the CPU, a few seconds with all cores): within the GEMM tolerance plus half a
+    bf16 ulp of the output, relative Frobenius error <= 6e-3 (each weight is rounded to
+    bf16 once, as the dequant kernel rounds it)."""
     m, k, n, group = 4096, 4096, 14336, 128
     a, w, s, z = operands(m, k, n, group, 0x5100)
     y_default, y_fused = run_both(rt, a, w, s, z, m, k, n, group, True)
     assert np.array_equal(y_default, y_fused)
+    y = oracle.bf16_to_f32(y_fused)
+    ref = oracle.w4a16_gemm(a, w, s, z, group, 8)
+    tol = oracle.gemm_tolerance(k, oracle.bf16_to_f32(a), oracle.dequant_qweight_f32(w, s, z, group, 8))
+    tol += float(np.abs(ref).max()) * 2.0 ** -8
+    err, rel = oracle.compare(y, ref)
+    assert np.isfinite(y).all() and err <= tol and rel <= 6e-3, (err, tol, rel)
 
 
 def test_ragged_fused_within_tolerance(rt):
