@@ -29,6 +29,28 @@ def test_library_exports_every_header_symbol():
     assert L.t0mi_abi_version() == 1
 
 
+def test_integration_rust_binding_covers_the_header():
+    """INTEGRATION.md's Rust `extern "C"` block declares every function of include/t0mi.h
+    exactly once, with as many parameters as the C declaration."""
+    text = open(os.path.join(ROOT, "include", "t0mi.h")).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    text = re.sub(r"//[^\n]*", "", text)
+    c_params = {}
+    for name, params in re.findall(r"\b(t0mi_[a-z0-9_]+)\s*\(([^;]*?)\)\s*;", text):
+        ps = [p for p in " ".join(params.split()).split(",") if p.strip() and p.strip() != "void"]
+        c_params[name] = len(ps)
+    doc = open(os.path.join(ROOT, "INTEGRATION.md")).read()
+    block = doc[doc.index('extern "C" {'):]
+    block = block[:block.index("\n}\n")]
+    rust = re.findall(r"pub fn (t0mi_[a-z0-9_]+)\(([^)]*)\)", block, flags=re.S)
+    names = [n for n, _ in rust]
+    assert len(names) == len(set(names)), "a function declared twice"
+    assert set(names) == set(c_params), (sorted(set(c_params) - set(names)), sorted(set(names) - set(c_params)))
+    for name, params in rust:
+        n = len([p for p in params.split(",") if p.strip()])
+        assert n == c_params[name], (name, n, c_params[name])
+
+
 def test_library_has_no_oracle_dependency():
     """The product must not link or embed the CPU oracle."""
     blob = open(t0mi.LIB_PATH, "rb").read()
