@@ -260,7 +260,6 @@ static double estimate_us(const t0mi_gemm_config& c, uint32_t m, uint32_t n, uin
   const double tm = ceil((double)m / c.tile_m), tn = ceil((double)n / c.tile_n);
   const double tiles = tm * tn * sk;
   const double wg_per_cu = wg_per_cu_of(c);
-  const double rounds = ceil(tiles / (CUS * wg_per_cu));
   const double kp = ceil((double)k / sk / c.tile_k) * c.tile_k;
   const double flops_tile = 2.0 * c.tile_m * c.tile_n * kp;
   const double busy = std::min(1.0, W * wg_per_cu / 4.0);
@@ -279,25 +278,39 @@ static double estimate_us(const t0mi_gemm_config& c, uint32_t m, uint32_t n, uin
   const double out_b = c.out_dtype == T0MI_OUT_BF16 ? 2.0 : 4.0;
   double hbm_bytes = 2.0 * m * k + 2.0 * k * n + (sk > 1 ? 0.0 : out_b) * m * n;
   const double l2_bytes = tiles * (c.tile_m + c.tile_n) * kp * 2.0;
-  // A CU streams its workgroups' tiles (and split-K planes) at ~55 GB/s through
-  // the LDS DMA of these kernels (measured: 128 x 4096 x 4096 with 128 x 128
-  // tiles, split-K 8 on 256 CUs streams 256 KB per CU in ~5 us; split-K 4 on
-  // 128 CUs, twice the bytes per CU, is ~2.4 us slower), so a grid that leaves
-  // CUs idle cannot reach the HBM rate.
-  const double R_CU = 55.0e9;
-  const double cu_bytes =
-      rounds * wg_per_cu * ((c.tile_m + c.tile_n) * kp * 2.0 + (sk > 1 ? c.tile_m * c.tile_n * 4.0 : 0.0));
+  // What one CU streams: its share of the workgroups, each its A and B panels
+  // over its K range and its split-K plane.  The rate a CU sustains through the
+  // LDS DMA of these kernels is set by the bytes it keeps in flight -- the
+  // workgroups resident on it at once, each with its LDS stages of a K tile --
+  // and saturates at ~50 GB/s: 5 + 0.4 GB/s per KB in flight.  Fitted to the
+  // times of every prebuilt candidate on 82 shapes (m = 1 .. 4096, N and K of
+  // 4096 .. 14336, both B layouts; B rotated over copies that exceed the
+  // Infinity Cache): with a fixed 55 GB/s per CU the model's pick came within
+  // 3 % of the fastest candidate on 31 of them, with this rate on 68.  It is
+  // what makes 128 x 128 tiles with four LDS stages and the many small
+  // workgroups of 64 x 64 / 64 x 128 tiles beat 128 x 256 tiles at 1-128 rows.
+  // Fewer resident waves than SIMDs issue the loads more slowly (single-wave
+  // 64 x 64 workgroups against four-wave ones of the same tile): the rate
+  // scales with the resident waves up to four (checked on 80 further shapes,
+  // N and K of 5120 .. 13824: picks within 3 % of the fastest on 55 of them
+  // against 38 for the fixed rate).
+  const double per_wg = (c.tile_m + c.tile_n) * kp * 2.0 + (sk > 1 ? c.tile_m * c.tile_n * 4.0 : 0.0);
+  const double wg_on_cu = std::min(wg_per_cu, ceil(tiles / CUS));
+  const double stages = std::max<uint32_t>(2u, c.stages);
+  const double in_flight_kb = wg_on_cu * stages * (c.tile_m + c.tile_n) * c.tile_k * 2.0 / 1024.0;
+  const double R_CU = std::min(50.0, 5.0 + 0.4 * in_flight_kb) * 1e9 * std::min(1.0, wg_on_cu * W / 4.0);
+  const double cu_bytes = ceil(tiles / CUS) * per_wg;
   const double t_mem = std::max({hbm_bytes / HBM, l2_bytes / L2, cu_bytes / R_CU});
   double t = std::max(t_comp, t_mem) * 1e6 + 3.0;
   // The split-K reduce pass is a separate launch: it reads every fp32 partial
-  // plane, just written and mostly served by the Infinity Cache (~12 TB/s:
-  // 16.8 MB in 4.2 us with its launch), and writes the output once.
-  if (sk > 1) t += (sk * 4.0 * m * n / 12.0e12 + out_b * m * n / HBM) * 1e6 + 3.0;
+  // plane, just written and mostly served by the Infinity Cache (~12 TB/s),
+  // and writes the output once.
+  if (sk > 1) t += (sk * 4.0 * m * n / 12.0e12 + out_b * m * n / HBM) * 1e6 + 2.0;
   // The split-K planes are stored after the K loops, all workgroups at once, so
-  // their write does not overlap the streaming of the operands (1024 x 4096 x
-  // 4096 with 256 x 256 tiles at split-K 4 writes 64 MB of planes: 47.8 us,
-  // against 43.3 us unsplit with 128 x 128 tiles).
-  if (sk > 1) t += sk * 4.0 * m * n / HBM * 1e6;
+  // their write does not overlap the streaming of the operands; fitted with the
+  // rate above at three times the plane bytes over the HBM rate (the write-back
+  // after the kernel and the reduce's first reads wait on it).
+  if (sk > 1) t += 3.0 * sk * 4.0 * m * n / HBM * 1e6;
   return t;
 }
 
