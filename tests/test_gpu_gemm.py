@@ -85,6 +85,23 @@ def test_integer_pattern_bf16_out_all_variants(rt, name, layout):
     assert np.array_equal(y, ref), f"{cfg.name()}: {np.count_nonzero(y != ref)} elements differ"
 
 
+PREBUILT = t0mi.variants()
+
+
+@pytest.mark.parametrize("idx", range(len(PREBUILT)))
+def test_every_prebuilt_kernel_integer_exact(rt, idx):
+    """Every kernel of the prebuilt table (tile, wave layout, LDS stages; each layout), also those
+    no preset names: ragged M and N, K not a multiple of tile_k, f32 out, equal to the exact
+    integer sums."""
+    cfg = PREBUILT[idx]
+    m, n, k = 200, 136, 264
+    a, b = int_pattern(m, k, n, cfg.transpose == t0mi.NN)
+    print(f"[prebuilt {idx}] {cfg.name()}", flush=True)
+    y = run_gemm(rt, cfg, a, b, m, n, k)
+    ref = oracle.gemm_bf16(a, b, "nn" if cfg.transpose == t0mi.NN else "nt")
+    assert np.array_equal(y, ref), f"{cfg.name()}: max diff {np.abs(y - ref).max()}"
+
+
 @pytest.mark.parametrize("layout", [t0mi.NT, t0mi.NN])
 @pytest.mark.parametrize("sk", [2, 4, 8])
 def test_split_k_exact_and_deterministic(rt, layout, sk):
