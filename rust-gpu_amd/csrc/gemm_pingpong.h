@@ -225,6 +225,12 @@ __global__ __launch_bounds__(512) void gemm_bf16_pingpong_kernel(GemmParams p) {
   const int nn_krow0 = X16 ? x16_krow(lane, 0) : 8 * (tg >> 1) + (ti >> 2);
   const int nn_col0 = wn * TN + (X16 ? x16_col(lane) : 16 * (tg & 1) + 4 * (ti & 3));
   const int nn_sw = swz_nn<NC, X16>(nn_krow0);
+  // Loop-invariant element offset of each block's transpose reads (k-row
+  // nn_krow0 of the tile, the block's columns): the k-step and half then go in
+  // the instruction's offset field, so a block's four reads share one address.
+  int nn_fo[FN];
+#pragma unroll
+  for (int fn = 0; fn < FN; ++fn) nn_fo[fn] = nn_krow0 * BN + nn_col_off(nn_col0 + fn * MB, nn_sw);
 
   bf16x8 xa[KS][FM], xb[KS][FN];
   i16x4 tr[KS][FN][2];
@@ -237,11 +243,8 @@ __global__ __launch_bounds__(512) void gemm_bf16_pingpong_kernel(GemmParams p) {
       xb[ks][r - FM] = *(const bf16x8*)(Bs + b_off[ks] + (r - FM) * MB * BK);
     } else {
       constexpr int fn = (r - FM) / 2, h = (r - FM) % 2;
-      const int col = nn_col0 + fn * MB;
-      const int eoff = nn_col_off(col, nn_sw);
-      const int krow = ks * (X16 ? 32 : 16) + 4 * h + nn_krow0;
       tr[ks][fn][h] = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-          (__attribute__((address_space(3))) i16x4*)(Bs + krow * BN + eoff));
+          (__attribute__((address_space(3))) i16x4*)(Bs + nn_fo[fn] + (ks * (X16 ? 32 : 16) + 4 * h) * BN));
       if constexpr (h == 1)
         xb[ks][fn] = __builtin_bit_cast(bf16x8, __builtin_shufflevector(tr[ks][fn][0], tr[ks][fn][1], 0, 1, 2, 3,
                                                                         4, 5, 6, 7));
@@ -268,8 +271,14 @@ __global__ __launch_bounds__(512) void gemm_bf16_pingpong_kernel(GemmParams p) {
   constexpr int NRD = KS * NR, RD = NRD / 8;
   auto read_phase = [&](int u, auto da_c, auto db_c) {
     constexpr bool DA = decltype(da_c)::value, DB = decltype(db_c)::value;
-    const uint16_t* As = a_slots + (u & 1) * AH_ELEMS;
-    const uint16_t* Bs = smem + (u % 3) * B_ELEMS;
+    // The ring slots as wave-uniform scalars: every fragment address is then
+    // one add of a loop-invariant lane offset and the slot, with the rest in
+    // the instruction's offset field.  (Left to the compiler, u % 3 is strength-
+    // reduced across iterations into two per-iteration terms, and the 16
+    // transpose reads took two VALU instructions each: 35 per read phase
+    // against 6, 2.7 % of the 4096^3 NN time.)
+    const uint16_t* As = a_slots + __builtin_amdgcn_readfirstlane((int)(u & 1)) * AH_ELEMS;
+    const uint16_t* Bs = smem + __builtin_amdgcn_readfirstlane((int)(u % 3)) * B_ELEMS;
     const char* b_tile = DB ? b_tile_of(u + 2) : nullptr;
     static_for<NRD>([&](auto ic) {
       constexpr int i = decltype(ic)::value;
