@@ -195,8 +195,11 @@ __global__ __launch_bounds__(512) void w4a16_pingpong_kernel(W4PPParams q) {
   // A fragments with one word dequantized after every second A read, so the
   // VALU work overlaps the A reads in flight and each word dies early.
   auto read_phase = [&](int u) {
-    const uint16_t* As = a_slots + (u & 1) * (AH_BYTES / 2);
-    const uint8_t* Bslot = smem + A_AREA + (u % 3) * BSLOT;
+    // Ring slots as wave-uniform scalars: each LDS address is then one add of
+    // a loop-invariant lane offset and the slot (u % 3 left to the compiler is
+    // strength-reduced across iterations into two per-iteration terms).
+    const uint16_t* As = a_slots + __builtin_amdgcn_readfirstlane((int)(u & 1)) * (AH_BYTES / 2);
+    const uint8_t* Bslot = smem + A_AREA + __builtin_amdgcn_readfirstlane((int)(u % 3)) * BSLOT;
     const uint32_t* Bw = (const uint32_t*)Bslot;
     static_for<KS * FN>([&](auto ic) {
       read_b(Bw, ic);
