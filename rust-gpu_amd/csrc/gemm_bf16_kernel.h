@@ -628,9 +628,13 @@ __device__ __forceinline__ void gemm_bf16_tile(const GemmParams& p, int tm, int 
   constexpr int PRE = SPREAD ? (LPT * (KS - 1) + KS - 1) / KS : 0;  // loads j with j*KS/LPT < KS-1
   auto iteration = [&](int it, auto barrier_c, auto load_c, auto check_c) {
     constexpr bool BARRIER = decltype(barrier_c)::value, LOAD = decltype(load_c)::value;
-    const uint16_t* cur = smem + (it % S) * BUF;
+    // Stages as wave-uniform scalars, so that each LDS address is one add of a
+    // loop-invariant lane offset and the stage (it % S left to the compiler is
+    // strength-reduced across iterations into several per-iteration terms).
+    const int cs = __builtin_amdgcn_readfirstlane(it % S);
+    const uint16_t* cur = smem + cs * BUF;
     const int lt = SPREAD ? it + S - 1 : it + S;          // tile loaded by this iteration
-    const int ls = SPREAD ? (it + S - 1) % S : it % S;    // its stage
+    const int ls = __builtin_amdgcn_readfirstlane(SPREAD ? (it + S - 1) % S : it % S);  // its stage
     static_for<KS - 1>([&](auto ksc) {
       constexpr int ks = decltype(ksc)::value;
       constexpr int c = ks & 1;
@@ -665,7 +669,7 @@ __device__ __forceinline__ void gemm_bf16_tile(const GemmParams& p, int tm, int 
         wait_vmcnt<0>();
       wait_lgkmcnt0();
       __syncthreads();
-      const uint16_t* nxt = smem + ((it + 1) % S) * BUF;
+      const uint16_t* nxt = smem + __builtin_amdgcn_readfirstlane((it + 1) % S) * BUF;
       constexpr int JL = SPREAD ? PRE : 0;
       constexpr int NDL = NDMA - JL;  // loads left for the last k-step
       constexpr int NMEM = NDL > NREAD ? NDL : NREAD;
