@@ -26,9 +26,9 @@
 //   group g, R(u): its A rows of tile u+1 and its half of B of tile u+2
 //   (group 0: A rows 0-127, NN B k-rows 8-15 of each 16, NT B rows 0-127;
 //    group 1: A rows 128-255, the other B k-rows / rows).
-// (NN moves one of its B loads into M(u); it goes to the same slot.)  A(u+1)
-// goes to the A slot the group read in R(u-1); B(u+2) to the B slot both
-// groups read in R(u-1), which the other group finished one interval before.  Waits (vmcnt counts a wave's DMA in issue order): at the end of
+// A(u+1) goes to the A slot the group read in R(u-1); B(u+2) to the B slot
+// both groups read in R(u-1), which the other group finished one interval
+// before.  Waits (vmcnt counts a wave's DMA in issue order): at the end of
 // R(u), for everything issued before R(u) -- B(u+1), which the other group
 // reads after the next barrier; at the end of M(u), for A(u+1), which the
 // group reads in R(u+1).  Each B half has two intervals to land, each A
@@ -264,10 +264,12 @@ __global__ __launch_bounds__(512) void gemm_bf16_pingpong_kernel(GemmParams p) {
   // B of tile u+2 for 4 <= j < 8 - BMM when DB) issued after read RD * j + 1;
   // then the reads are waited for, and this wave's DMA issued before R(u)
   // (its B half of tile u+1): vmcnt may keep only the loads issued here.
-  // BMM: B loads issued from the MFMA phase instead -- each stalls the MFMA
-  // stream for ~26 cycles, so only NN (whose read phase, with its transpose
-  // reads, is the longer one) moves one there.
-  constexpr int BMM = NN && X16 ? 1 : 0;
+  // BMM: B loads issued from the MFMA phase instead.  Each stalls the MFMA
+  // stream for ~26 cycles; with one add per fragment address every read phase
+  // ends well inside the other group's MFMA phase (NN ~800 of ~1080 cycles), so
+  // all loads stay in the read phases (one NN load in the MFMA phase measured
+  // 0.8 % slower at 4096^3).  Kept as a parameter for read phases that grow.
+  constexpr int BMM = 0;
   constexpr int NRD = KS * NR, RD = NRD / 8;
   auto read_phase = [&](int u, auto da_c, auto db_c) {
     constexpr bool DA = decltype(da_c)::value, DB = decltype(db_c)::value;
