@@ -37,15 +37,24 @@ extern "C" int t0mi_gptq_parse(const void* raw, size_t len, t0mi_gptq_info* out)
     return set_error(T0MI_ERR_INVALID, "GPTQ rows * cols = %llu is odd (two INT4 values per byte)",
                      (unsigned long long)info.rows * info.cols);
   info.n_groups = info.cols / info.group_size;
-  const uint64_t n_params = (uint64_t)info.n_groups * info.rows;
+  const uint64_t n_params = (uint64_t)info.n_groups * info.rows;  // < 2^64: both factors < 2^32
   info.packed_offset = 12;
   info.packed_bytes = (uint64_t)info.rows * info.cols / 2;
+  // The section sizes can pass 2^64 bytes for header values near 2^32 (n_params * 8
+  // wraps), so the length check is made in 128-bit arithmetic before any offset
+  // is formed: a wrapped total would let the scan below read past the buffer.
+  const unsigned __int128 total =
+      (unsigned __int128)info.packed_offset + info.packed_bytes + (unsigned __int128)n_params * 8u;
+  if (total > (unsigned __int128)len) {
+    if (total >> 64)
+      return set_error(T0MI_ERR_INVALID, "GPTQ data truncated: the header (rows %u, cols %u, group %u) needs "
+                       "more than 2^64 bytes, got %zu", info.rows, info.cols, info.group_size, len);
+    return set_error(T0MI_ERR_INVALID, "GPTQ data truncated: need %llu bytes, got %zu",
+                     (unsigned long long)total, len);
+  }
   info.scales_offset = info.packed_offset + info.packed_bytes;
   info.zeros_offset = info.scales_offset + n_params * 4;
   info.total_bytes = info.zeros_offset + n_params * 4;
-  if (len < info.total_bytes)
-    return set_error(T0MI_ERR_INVALID, "GPTQ data truncated: need %llu bytes, got %zu",
-                     (unsigned long long)info.total_bytes, len);
   info.zeros_in_range = 1;
   info.scales_bf16_exact = 1;
   for (uint64_t i = 0; i < n_params; ++i) {

@@ -60,6 +60,45 @@ def test_from_bytes_rejects_where_the_reference_panics(raw, why):
     assert e.value.code == t0mi.ERR_INVALID and why in str(e.value)
 
 
+@pytest.mark.parametrize("rows,cols,group", [
+    (1589614079, 4095720868, 1),   # sections total 3 * 2^64 + 26 bytes: wrapped, 26 looked valid
+    (0xFFFFFFFE, 0xFFFFFFFF, 1),   # n_groups * rows * 8 bytes of sections: past 2^64
+    (0xFFFFFFFE, 0xFFFFFFFE, 2),
+    (0x80000000, 0xFFFFFFFF, 1),
+    (0xFFFFFFFE, 64, 1),           # large but below 2^64: plainly truncated
+])
+def test_header_sizes_past_the_buffer_are_refused(rows, cols, group):
+    """Header values near 2^32 make the section sizes reach or pass 2^64 bytes; the
+    parser must refuse them as truncated (checked before any section is read), not
+    wrap the total and scan past the buffer.  The first header's total wraps to 26
+    bytes, which 64-bit arithmetic accepted for this 4108-byte buffer, and the flag
+    scan then read ~3e18 bytes past it."""
+    raw = struct.pack("<3I", rows, cols, group) + bytes(4096)
+    with pytest.raises(t0mi.T0miError) as e:
+        t0mi.GptqWeight.from_bytes(raw)
+    assert e.value.code == t0mi.ERR_INVALID and "truncated" in str(e.value)
+
+
+def test_random_headers_parse_or_refuse():
+    """Seeded random headers over short buffers: every call either parses with all
+    sections inside the buffer or raises T0miError (no other outcome)."""
+    rng = np.random.default_rng(0x6707)
+    for _ in range(2000):
+        rows, cols, group = (int(v) for v in rng.integers(0, 2**32, size=3, dtype=np.uint64))
+        if rng.random() < 0.5:
+            rows, cols = rows % 64, cols % 64
+            group = group % 70
+        body = rng.integers(0, 256, size=int(rng.integers(0, 600)), dtype=np.uint8).tobytes()
+        raw = struct.pack("<3I", rows, cols, group) + body
+        try:
+            g = t0mi.GptqWeight.from_bytes(raw)
+        except t0mi.T0miError as e:
+            assert e.code == t0mi.ERR_INVALID
+            continue
+        assert g.info.total_bytes <= len(raw)
+        assert g.info.total_bytes == 12 + rows * cols // 2 + 8 * (cols // group) * rows
+
+
 def test_odd_element_count_is_an_error():
     """rows * cols odd: two INT4 values per byte cannot hold it (the reference's
     rows * cols / 2 would drop the last nibble)."""
