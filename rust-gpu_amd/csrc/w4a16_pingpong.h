@@ -21,12 +21,14 @@
 // What differs from the bf16 GEMM: the B tile is DMA'd as packed words (8 rows
 // of 256 words = 8 KB per 64-K tile instead of 32 KB of bf16).  In the NN MFMA
 // operand layout a lane's 8 consecutive k values of one column are exactly one
-// packed word, so each B fragment is one ds_read_b32 plus ~23 VALU
-// instructions in the read phase: nibbles spread to bytes (2 AND/shift),
-// v_cvt_f32_ubyte0..3, one fma q*s + (-z*s) (exact: |q - z| < 16 and s has 8
-// significant bits) and v_cvt_pk_bf16_f32 (RNE).  The read phase has the slack
-// for it (the MFMA phase is the longer of the two).  Each tile's 256 scales
-// and 32 zero words travel with its packed words (DMA into the same LDS slot).
+// packed word, so a B fragment is one ds_read_b32 plus ~23 VALU instructions:
+// nibbles spread to bytes (2 AND/shift), v_cvt_f32_ubyte0..3, one fma
+// q*s + (-z*s) (exact: |q - z| < 16 and s has 8 significant bits) and
+// v_cvt_pk_bf16_f32 (RNE).  Both groups multiply the same B tile (by their own
+// 128 rows of A), so each word is dequantized once per workgroup, half of each
+// tile by either group in its read phase, and the other group reads those
+// fragments back from LDS as bf16.  Each tile's 256 scales and 32 zero words
+// travel with its packed words (DMA into the same LDS slot).
 //
 // Preconditions (w4_pingpong_ok): K and the split-K partition length are
 // multiples of 64 and the group a multiple of 64, so every 64-K tile lies in
@@ -93,7 +95,8 @@ __global__ __launch_bounds__(512) void w4a16_pingpong_kernel(W4PPParams q) {
   // out-of-range lanes of those two DMAs write.
   constexpr int BROW = 1152, SZ = 8 * BROW, BSLOT = SZ + 2048;
   constexpr int A_AREA = 4 * AH_BYTES;  // two groups x two slots
-  constexpr int LDS_BYTES = A_AREA + 3 * BSLOT > 8 * 16384 ? A_AREA + 3 * BSLOT : 8 * 16384;  // staged store reuses it
+  constexpr int XB_OFF = A_AREA + 3 * BSLOT;  // dequantized fragments: F (16 KB), then S (16 KB)
+  constexpr int LDS_BYTES = XB_OFF + 32768 > 8 * 16384 ? XB_OFF + 32768 : 8 * 16384;  // staged store reuses it
   __shared__ __attribute__((aligned(1024))) uint8_t smem[LDS_BYTES];
 
   int tm, tn, part;
@@ -168,17 +171,17 @@ __global__ __launch_bounds__(512) void w4a16_pingpong_kernel(W4PPParams q) {
   for (int ks = 0; ks < KS; ++ks) a_off[ks] = lrow * BK + (((ks * 2 + lhalf) ^ swz<KC>(lrow)) * 8);
   bf16x8 xa[KS][FM], xb[KS][FN];
   uint32_t bw[KS][FN];
-  // A fragment i (k-step i / FM, row block i % FM); B word i (k-step i / FN,
-  // column block i % FN).
+  // A fragment i (k-step i / FM, row block i % FM).
   auto read_a = [&](const uint16_t* As, auto ic) {
     constexpr int i = decltype(ic)::value;
     xa[i / FM][i % FM] = *(const bf16x8*)(As + a_off[i / FM] + (i % FM) * 32 * BK);
   };
-  // B word of k-step ks, column block fn: a lane base plus an immediate.
+  // Packed B word i of k-steps K0.. (k-step K0 + i / FN, column block i % FN):
+  // a lane base plus an immediate.
   const int b_lane = lhalf * (BROW / 4) + wn * TN + lrow;  // in words
-  auto read_b = [&](const uint32_t* Bw, auto ic) {
+  auto read_b = [&](const uint32_t* Bw, auto k0c, auto ic) {
     constexpr int i = decltype(ic)::value;
-    constexpr int ks = i / FN, fn = i % FN;
+    constexpr int ks = decltype(k0c)::value + i / FN, fn = i % FN;
     bw[ks][fn] = Bw[b_lane + ks * 2 * (BROW / 4) + fn * 32];
   };
 
@@ -191,41 +194,106 @@ __global__ __launch_bounds__(512) void w4a16_pingpong_kernel(W4PPParams q) {
       for (int r = 0; r < 16; ++r) acc[fn][fm][r] = 0.0f;
 
   const uint16_t* a_slots = (const uint16_t*)(smem + g * 2 * AH_BYTES);
-  // R(u): tile u's 8 packed B words and its scales / zero points, then its 16
-  // A fragments with one word dequantized after every second A read, so the
-  // VALU work overlaps the A reads in flight and each word dies early.
-  auto read_phase = [&](int u) {
-    // Ring slots as wave-uniform scalars: each LDS address is then one add of
-    // a loop-invariant lane offset and the slot (u % 3 left to the compiler is
-    // strength-reduced across iterations into two per-iteration terms).
-    const uint16_t* As = a_slots + __builtin_amdgcn_readfirstlane((int)(u & 1)) * (AH_BYTES / 2);
-    const uint8_t* Bslot = smem + A_AREA + __builtin_amdgcn_readfirstlane((int)(u % 3)) * BSLOT;
-    const uint32_t* Bw = (const uint32_t*)Bslot;
-    static_for<KS * FN>([&](auto ic) {
-      read_b(Bw, ic);
-      __builtin_amdgcn_sched_barrier(0);
-    });
-    float s_t[2], cz_t[2];
-    uint32_t sraw[2], zraw[2];
+  // Dequantized B fragments shared by the two groups, so that each packed word
+  // is dequantized once per workgroup: region F holds k-steps 0-1 of a tile,
+  // dequantized by group 1 in its read phase of the previous tile (their packed
+  // rows 0-3 are group 0's DMA, landed a phase earlier), region S k-steps 2-3,
+  // dequantized by group 0 in its read phase of the tile and read by group 1 in
+  // the next phase.  Fragment (ks, fn) of column block wn lies at
+  // XB_OFF + wn * 4 KB + ((ks % 2) * 2 + fn) KB (+ 16 KB for S), 16 bytes per
+  // lane; only the waves of column block wn touch it, and one barrier separates
+  // every write from its reads and every read from the next write.
+  uint8_t* const xf = smem + XB_OFF + wn * 4096 + lane * 16;
+  uint8_t* const xs = xf + 16384;
+  auto frag = [](uint8_t* base, int ks, int fn) -> bf16x8* { return (bf16x8*)(base + ((ks & 1) * 2 + fn) * 1024); };
+  // The lane's two columns' scales and zero points of a tile (issue, then after
+  // the wait -z * s, exact: z < 16 and s has 8 significant bits).
+  uint32_t sraw[2], zraw[2];
+  float s_t[2], cz_t[2];
+  auto sz_read = [&](const uint8_t* Bslot) {
 #pragma unroll
     for (int f = 0; f < 2; ++f) {
       sraw[f] = ((const uint16_t*)(Bslot + SZ))[wn * TN + f * 32 + lrow];
       if constexpr (ZEROS) zraw[f] = ((const uint32_t*)(Bslot + SZ + 1024))[(wn * TN + f * 32 + lrow) / 8];
     }
-    __builtin_amdgcn_sched_barrier(0);
-    wait_lgkmcnt0();
+  };
+  auto sz_math = [&]() {
 #pragma unroll
     for (int f = 0; f < 2; ++f) {
       s_t[f] = __builtin_bit_cast(float, sraw[f] << 16);
       const float z = ZEROS ? (float)((zraw[f] >> (4 * (lrow & 7))) & 0xFu) : (float)q.zp_const;
-      cz_t[f] = -z * s_t[f];  // exact: z < 16, s has 8 significant bits
+      cz_t[f] = -z * s_t[f];
     }
+  };
+  // Ring slots as wave-uniform scalars: each LDS address is then one add of a
+  // loop-invariant lane offset and the slot (u % 3 left to the compiler is
+  // strength-reduced across iterations into two per-iteration terms).
+  auto a_slot = [&](int u) { return a_slots + __builtin_amdgcn_readfirstlane((int)(u & 1)) * (AH_BYTES / 2); };
+  auto b_slot = [&](int u) { return smem + A_AREA + __builtin_amdgcn_readfirstlane((int)(u % 3)) * BSLOT; };
+  // R(u), group 0: the packed words of k-steps 2-3 and the F fragments of
+  // k-steps 0-1, then tile u's 16 A fragments with one word dequantized (into
+  // xb and S) after every fourth A read, so the VALU work overlaps the A reads
+  // in flight.
+  auto read_phase_g0 = [&](int u) {
+    const uint16_t* As = a_slot(u);
+    const uint8_t* Bslot = b_slot(u);
+    const uint32_t* Bw = (const uint32_t*)Bslot;
+    static_for<4>([&](auto ic) {
+      read_b(Bw, std::integral_constant<int, 2>{}, ic);
+      __builtin_amdgcn_sched_barrier(0);
+    });
+    static_for<4>([&](auto ic) {
+      constexpr int i = decltype(ic)::value, ks = i / FN, fn = i % FN;
+      xb[ks][fn] = *frag(xf, ks, fn);
+      __builtin_amdgcn_sched_barrier(0);
+    });
+    sz_read(Bslot);
+    __builtin_amdgcn_sched_barrier(0);
+    wait_lgkmcnt0();
+    sz_math();
     static_for<KS * FM>([&](auto ic) {
       constexpr int i = decltype(ic)::value;
       read_a(As, ic);
-      if constexpr (i % 2 == 1) {
-        constexpr int wi = i / 2, ks = wi / FN, fn = wi % FN;
+      if constexpr (i % 4 == 1) {
+        constexpr int wi = i / 4, ks = 2 + wi / FN, fn = wi % FN;
         xb[ks][fn] = dequant_word(bw[ks][fn], s_t[fn], cz_t[fn]);
+        *frag(xs, ks, fn) = xb[ks][fn];
+      }
+      __builtin_amdgcn_sched_barrier(0);
+    });
+    wait_lgkmcnt0();
+  };
+  // R(u), group 1: tile u's 8 fragments from F and S and, when tile u+1
+  // exists (NX), its packed words of k-steps 0-1 and its scales; after the
+  // wait (which also lets the F reads return before F is rewritten) tile u's
+  // 16 A fragments with one of tile u+1's words dequantized into F after every
+  // fourth A read.
+  auto read_phase_g1 = [&](int u, auto nx_c) {
+    constexpr bool NX = decltype(nx_c)::value;
+    const uint16_t* As = a_slot(u);
+    static_for<KS * FN>([&](auto ic) {
+      constexpr int i = decltype(ic)::value, ks = i / FN, fn = i % FN;
+      xb[ks][fn] = *frag(ks < 2 ? xf : xs, ks, fn);
+      __builtin_amdgcn_sched_barrier(0);
+    });
+    if constexpr (NX) {
+      const uint8_t* Bslot = b_slot(u + 1);
+      const uint32_t* Bw = (const uint32_t*)Bslot;
+      static_for<4>([&](auto ic) {
+        read_b(Bw, std::integral_constant<int, 0>{}, ic);
+        __builtin_amdgcn_sched_barrier(0);
+      });
+      sz_read(Bslot);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    wait_lgkmcnt0();
+    if constexpr (NX) sz_math();
+    static_for<KS * FM>([&](auto ic) {
+      constexpr int i = decltype(ic)::value;
+      read_a(As, ic);
+      if constexpr (NX && i % 4 == 1) {
+        constexpr int wi = i / 4, ks = wi / FN, fn = wi % FN;
+        *frag(xf, ks, fn) = dequant_word(bw[ks][fn], s_t[fn], cz_t[fn]);
       }
       __builtin_amdgcn_sched_barrier(0);
     });
@@ -256,7 +324,8 @@ __global__ __launch_bounds__(512) void w4a16_pingpong_kernel(W4PPParams q) {
   // behind), with the DMA of tile u+2 (with its scales and zero points) inside
   // M(u) -- between 32-cycle MFMAs a DMA issue does not stall the MFMA stream,
   // and the read phase carries the dequant -- each wave waiting for its DMA at
-  // the end of its next read phase.
+  // the end of its next read phase.  Before group 0's first read phase group 1
+  // dequantizes tile 0's k-steps 0-1 into F (one extra barrier for both groups).
   if (nk > 0) {
     static_for<NDMA>([&](auto jc) { dma(0, jc); });
     if (wave == 0) dma_sz(0);
@@ -267,22 +336,46 @@ __global__ __launch_bounds__(512) void w4a16_pingpong_kernel(W4PPParams q) {
   }
   wait_vmcnt<0>();
   bar();
+  if (!g0 && nk > 0) {
+    const uint8_t* Bslot = b_slot(0);
+    const uint32_t* Bw = (const uint32_t*)Bslot;
+    static_for<4>([&](auto ic) { read_b(Bw, std::integral_constant<int, 0>{}, ic); });
+    sz_read(Bslot);
+    wait_lgkmcnt0();
+    sz_math();
+    static_for<4>([&](auto ic) {
+      constexpr int i = decltype(ic)::value, ks = i / FN, fn = i % FN;
+      *frag(xf, ks, fn) = dequant_word(bw[ks][fn], s_t[fn], cz_t[fn]);
+    });
+    wait_lgkmcnt0();
+  }
+  bar();
   if (!g0) bar();
-  int u = 0;
-  for (; u + 2 < nk; ++u) {
-    read_phase(u);
-    wait_vmcnt<0>();
-    bar();
-    mfma_phase(True{}, u + 2);
-    bar();
-  }
-  for (; u < nk; ++u) {
-    read_phase(u);
-    wait_vmcnt<0>();
-    bar();
-    mfma_phase(False{}, 0);
-    if (u + 1 < nk) bar();
-  }
+  // Each group runs its own copy of the loops (a wave-uniform branch taken once
+  // instead of once per read phase); both execute the same barriers.
+  auto run = [&](auto g0_c) {
+    constexpr bool G0 = decltype(g0_c)::value;
+    int u = 0;
+    for (; u + 2 < nk; ++u) {
+      if constexpr (G0) read_phase_g0(u);
+      else read_phase_g1(u, True{});
+      wait_vmcnt<0>();
+      bar();
+      mfma_phase(True{}, u + 2);
+      bar();
+    }
+    for (; u < nk; ++u) {
+      if constexpr (G0) read_phase_g0(u);
+      else if (u + 1 < nk) read_phase_g1(u, True{});
+      else read_phase_g1(u, False{});
+      wait_vmcnt<0>();
+      bar();
+      mfma_phase(False{}, 0);
+      if (u + 1 < nk) bar();
+    }
+  };
+  if (g0) run(True{});
+  else run(False{});
   if (g0) bar();
 
   // ---- epilogue --------------------------------------------------------------
