@@ -345,7 +345,8 @@ static int hip_fail(hipError_t e, const char* what) {
 //    the weights are dequantized once to bf16 and the dense NN GEMM runs: the
 //    dequant pass (0.5 B read + 2 B written per weight, at HBM speed) then costs
 //    less than dequantizing inside every M tile's K-loop, which is VALU work
-//    (2048 rows: 224 us two-pass against 232 us fused; 4096 rows: 414 vs 457);
+//    (N = 14336: 2048 rows 193 us two-pass against 208 us fused; 4096 rows 357
+//    against 420);
 //    and from kSplitRouteRows + 1 rows on when the fused kernel's tiles overflow
 //    one round and the dense GEMM's plan splits the columns.
 static constexpr uint32_t kDecodeMaxRows = 80;    // groups the one-slab decode kernels take
